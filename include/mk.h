@@ -1,0 +1,248 @@
+/*
+ * mk.h — C-ABI of libmk, the MI355X (gfx950) compute core behind mKernel's
+ * fused operators at one GPU's share of the work.
+ *
+ * Plain pointers and sizes only; no torch types.  Every device pointer is a
+ * HIP device address; `stream` is a hipStream_t passed as void* (NULL = the
+ * default stream).  All tensors are caller-owned and row-major.  bf16 buffers
+ * are raw 16-bit storage (IEEE bfloat16).
+ *
+ * Return codes: 0 = ok, negative = argument/shape error (MK_E*), positive =
+ * a hipError_t from a launch.  mk_last_error_string() describes the last
+ * non-zero return on the calling thread.
+ *
+ * Each entry point names the reference interface it replaces (file:line in
+ * uccl-project/mKernel).
+ */
+#ifndef MK_H_
+#define MK_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MK_OK 0
+#define MK_EINVAL (-1)   /* null pointer / bad enum */
+#define MK_ESHAPE (-2)   /* shape not supported by the tiling */
+#define MK_EDEVICE (-3)  /* no usable device / wrong architecture */
+#define MK_ETIMEOUT (-4) /* a bounded flag wait expired (error word set) */
+
+#define MK_ROW_BLOCK 128 /* flag / expert-padding granularity (rows) */
+
+/* ------------------------------------------------------------------------ */
+/* Plain persistent bf16 GEMM: C[M,N] = A[M,K] @ B[K,N], fp32 accumulate,
+ * bf16 (round-to-nearest-even) output.
+ * Replaces the compute role shared by ag_gemm / gemm_rs
+ * (reference src/gemm_rs.cu:36-114 compute_tile_impl,
+ *  src/ag_gemm.cu:265-461 fused_comp_sm).
+ * Requires M % 128 == 0, N % 256 == 0, K % 64 == 0, ld* >= row width and
+ * ld* % 8 == 0. */
+typedef struct mk_gemm_args {
+  const void* A;  /* bf16 [M, lda] */
+  const void* B;  /* bf16 [K, ldb] */
+  void* C;        /* bf16 [M, ldc] */
+  int64_t M, N, K;
+  int64_t lda, ldb, ldc;
+  int32_t num_cus; /* persistent grid size; 0 = every CU of the device */
+  int32_t tile_m;  /* 0 = auto, else 128 or 256 */
+} mk_gemm_args;
+int mk_gemm(const mk_gemm_args* args, void* stream);
+
+/* ------------------------------------------------------------------------ */
+/* Flag-gated AllGather+GEMM consumer with an in-GPU producer role.
+ * C[M,N] = A_full[M,K] @ B[K,N].  A_full is assembled from `world` row
+ * shards: `num_producers` producer workgroups copy 128-row tiles of
+ * A_shards into A_full in the order `stage_order` and release-store
+ * flags[tile] = epoch after each tile; compute workgroups acquire-poll the
+ * flags of the rows they are about to read (s_sleep between polls).
+ * Replaces ag_gemm_multinode::entrypoint
+ * (reference include/operators/ag_gemm/ag_gemm.cuh:362-509) with the
+ * intra_comm_sm gather role (src/ag_gemm.cu:31-215) and the per-chunk flag
+ * wait of fused_comp_sm (src/ag_gemm.cu:374-377).
+ *   gated == 0             : plain GEMM on A_full, no flags read (baseline)
+ *   gated, producers == 0  : flags are published by someone else
+ *   gated, producers  > 0  : producer role runs inside the same launch     */
+typedef struct mk_ag_gemm_args {
+  const void* A_shards;  /* bf16 [M, K]: shards stacked in rank order (source) */
+  void* A_full;          /* bf16 [M, K]: gathered A (destination / GEMM input) */
+  const void* B;         /* bf16 [K, N] */
+  void* C;               /* bf16 [M, N] */
+  int64_t M, N, K;
+  uint32_t* flags;              /* [M/128] epoch-stamped ready flags */
+  const int32_t* stage_order;   /* [M/128] device; NULL = ascending */
+  uint32_t epoch;               /* value a ready flag must hold (never 0) */
+  int32_t gated;
+  int32_t num_producers;
+  int32_t num_cus;              /* total workgroups (producers + compute); 0 = all CUs */
+  uint32_t spin_limit;          /* polls before a wait gives up; 0 = unbounded */
+  uint32_t* error_word;         /* optional device word, bit0 set on timeout */
+} mk_ag_gemm_args;
+int mk_ag_gemm(const mk_ag_gemm_args* args, void* stream);
+
+/* ------------------------------------------------------------------------ */
+/* GEMM + reduce-scatter epilogue at one rank's share.
+ * P = A[M,K] @ B[K,N] (this rank's partial over all M rows).  Rows owned by
+ * `rank` ([rank*M/world, (rank+1)*M/world)) are folded in the epilogue:
+ *   output = bf16( P_owned + sum_{p<world-1} peer_recv[p] )   (fp32 adds)
+ * after acquire-waiting the flags of each peer tile; every other row is the
+ * would-be send and is written to workspace.  The producer role copies
+ * peer_src into peer_recv tile by tile and release-stores the flags.
+ * Replaces gemm_rs_multinode::entrypoint_fused
+ * (reference include/operators/gemm_rs/gemm_rs.cuh:510-935): compute_tile_impl
+ * (src/gemm_rs.cu:36-114) + reduce_tiles_ws (src/gemm_rs.cu:685-845). */
+typedef struct mk_gemm_rs_args {
+  const void* A;          /* bf16 [M, K] */
+  const void* B;          /* bf16 [K, N] */
+  void* workspace;        /* bf16 [M, N]; non-owned rows written */
+  void* output;           /* bf16 [M/world, N] owned slice */
+  const void* peer_src;   /* bf16 [world-1, M/world, N] partials to stage */
+  void* peer_recv;        /* bf16 [world-1, M/world, N] staged partials */
+  int64_t M, N, K;
+  int32_t world, rank;
+  uint32_t* flags;              /* [(world-1) * (M/world)/128] */
+  const int32_t* stage_order;   /* [(world-1) * (M/world)/128]; NULL = ascending */
+  uint32_t epoch;
+  int32_t gated;
+  int32_t num_producers;
+  int32_t num_cus;
+  uint32_t spin_limit;
+  uint32_t* error_word;
+} mk_gemm_rs_args;
+int mk_gemm_rs(const mk_gemm_rs_args* args, void* stream);
+
+/* ------------------------------------------------------------------------ */
+/* MoE routing index build (host memory, host CPU).  Restates the reference's
+ * host-side builders bench/dispatch_gemm_bench.py:127-188 (build_routing,
+ * build_pull_indices) and bench/dispatch_gemm_glu_combine_bench.py:222-293,
+ * 513-527 (build_gather_indices, local_rb_per_expert, row_expert) for one
+ * rank owning experts [expert_begin, expert_begin + n_local).
+ * Rows are grouped by local expert (ascending); inside an expert, source
+ * tokens ascend; each expert is padded to a multiple of `row_block` with
+ * pull rows (-1,-1,-1).  Tokens come from one source (node 0, dev 0). */
+int mk_moe_index_sizes(const int32_t* topk_ids, int32_t num_tokens, int32_t topk,
+                       int32_t expert_begin, int32_t n_local, int32_t row_block,
+                       int64_t* R_out, int64_t* R_pad_out);
+
+typedef struct mk_moe_index {
+  /* all host arrays, caller-allocated */
+  int32_t* padded_tokens_per_expert; /* [n_local] */
+  int32_t* local_rb_per_expert;      /* [n_local] whole row blocks of real rows */
+  int32_t* pull_indices;             /* [R_pad, 3] (src_node, src_dev, src_token) */
+  int32_t* row_expert;               /* [R_pad] local expert of each row */
+  int32_t* rb_expert;                /* [R_pad / row_block] */
+  float* row_weight;                 /* [R_pad] gate of each row; 0 on padding */
+  int32_t* owner_offset;             /* [num_tokens + 1] CSR over source tokens */
+  int32_t* row_to_slot;              /* [R_pad] slot of each row; 0 on padding */
+  int32_t* row_to_owner;             /* [R_pad] owner dev of each row; -1 on padding */
+  int32_t* slot_to_row;              /* [R] inverse of row_to_slot */
+} mk_moe_index;
+int mk_moe_build_indices(const int32_t* topk_ids, const float* topk_gates,
+                         int32_t num_tokens, int32_t topk, int32_t expert_begin,
+                         int32_t n_local, int32_t row_block, const mk_moe_index* out);
+
+/* Token permute into expert-contiguous rows:
+ *   post[r] = tokens[src_row(r)]   (bit-exact copy), zero on padding rows,
+ * src_row = (src_node * devs_per_node + src_dev) * tokens_per_src + src_token.
+ * Replaces dispatch_fused (reference src/dispatch_gemm.cu:106-198). */
+typedef struct mk_moe_permute_args {
+  const void* tokens;           /* bf16 [n_src_rows, H] */
+  const int32_t* pull_indices;  /* [R_pad, 3] device */
+  void* post_tokens;            /* bf16 [R_pad, H] */
+  int64_t R_pad, H;
+  int64_t n_src_rows;
+  int32_t tokens_per_src, devs_per_node;
+} mk_moe_permute_args;
+int mk_moe_permute(const mk_moe_permute_args* args, void* stream);
+
+/* Grouped GEMM over expert-contiguous rows.
+ *   mode 0: out[r] = post[r] @ W[e(r)]                 (W: [E, K, N])
+ *   mode 1: out[r] = silu(h[:, :I]) * h[:, I:], h = post[r] @ W[e(r)]
+ *           (W: [E, K, 2I], out: [R_pad, I])   SwiGLU fused in the epilogue
+ * e(r) = rb_expert[r / 128] when rb_expert is given, else the expert whose
+ * padded row range [sum_{e'<e} padded[e'], sum_{e'<=e} padded[e']) holds r,
+ * from padded_tokens_per_expert (the reference's own table).
+ * Replaces group_gemm_fused (reference src/dispatch_gemm.cu:207-408),
+ * gemm1_swiglu_fused (src/dispatch_gemm_glu_combine.cu:441-643) and
+ * ffn_gemm2/grouped_gemm (src/dispatch_gemm_glu_combine.cu:247-429,647-651). */
+typedef struct mk_moe_grouped_gemm_args {
+  const void* A;              /* bf16 [R_pad, K] */
+  const void* W;              /* bf16 [E, K, Nw] */
+  void* out;                  /* bf16 [R_pad, N_out] */
+  const int32_t* rb_expert;   /* [R_pad/128] device, or NULL */
+  const int32_t* padded_tokens_per_expert; /* [E] device; used when rb_expert is NULL */
+  int64_t R_pad, K, Nw;       /* Nw = W's column count (2I in mode 1) */
+  int32_t num_experts;
+  int32_t mode;
+  int32_t num_cus;
+} mk_moe_grouped_gemm_args;
+int mk_moe_grouped_gemm(const mk_moe_grouped_gemm_args* args, void* stream);
+
+/* Top-k weighted combine back to source-token order (gather, no atomics):
+ *   y[t] = sum_{s in [owner_offset[t], owner_offset[t+1])}
+ *              row_weight[slot_to_row[s]] * y_expert[slot_to_row[s]]
+ * products and sum in fp32; output fp32 (out_dtype 0) or bf16 (1).
+ * Replaces combine_producer_fused + combine_gather_owner
+ * (reference src/dispatch_gemm_glu_combine.cu:736-818). */
+typedef struct mk_moe_combine_args {
+  const void* y_expert;         /* bf16 [R_pad, H] */
+  const float* row_weight;      /* [R_pad] */
+  const int32_t* owner_offset;  /* [num_tokens + 1] */
+  const int32_t* slot_to_row;   /* [R] */
+  void* y_out;                  /* [num_tokens, H] fp32 or bf16 */
+  int64_t num_tokens, H;
+  int32_t out_dtype;
+} mk_moe_combine_args;
+int mk_moe_combine(const mk_moe_combine_args* args, void* stream);
+
+/* slot_to_row[row_to_slot[r]] = r for every row with row_to_owner[r] >= 0:
+ * turns the reference's producer-side table (row_to_slot) into the gather
+ * table the combine reads. */
+int mk_moe_invert_slots(const int32_t* row_to_slot, const int32_t* row_to_owner, int64_t R_pad,
+                        int32_t* slot_to_row, void* stream);
+
+/* The whole local MoE layer in one call: permute -> grouped GEMM1 + SwiGLU ->
+ * grouped GEMM2 -> combine (four launches on `stream`).
+ * Replaces moe_dispatch_gemm_glu_combine_fused
+ * (reference include/operators/dispatch_gemm_glu_combine/dispatch_gemm_glu_combine.cuh:307-548). */
+typedef struct mk_moe_ffn_args {
+  const void* tokens;           /* bf16 [n_src_rows, H] */
+  const int32_t* pull_indices;  /* [R_pad, 3] */
+  const int32_t* rb_expert;     /* [R_pad/128], or NULL */
+  const int32_t* padded_tokens_per_expert; /* [E]; used when rb_expert is NULL */
+  const float* row_weight;      /* [R_pad] */
+  const int32_t* owner_offset;  /* [num_tokens + 1] */
+  const int32_t* slot_to_row;   /* [R] */
+  const void* w1;               /* bf16 [E, H, 2I] (gate | up) */
+  const void* w2;               /* bf16 [E, I, H] */
+  void* post_tokens;            /* bf16 [R_pad, H]  (caller scratch / output) */
+  void* act;                    /* bf16 [R_pad, I] */
+  void* y_expert;               /* bf16 [R_pad, H] */
+  void* y_out;                  /* [num_tokens, H] fp32 or bf16 */
+  int64_t num_tokens, n_src_rows, R_pad, H, I;
+  int32_t num_experts;
+  int32_t tokens_per_src, devs_per_node;
+  int32_t out_dtype;
+  int32_t num_cus;
+} mk_moe_ffn_args;
+int mk_moe_ffn_combine(const mk_moe_ffn_args* args, void* stream);
+
+/* ------------------------------------------------------------------------ */
+/* Scratch sizes.  Every entry point above works on caller buffers only; this
+ * reports 0 for all of them and exists so callers can size a workspace the
+ * same way for future kernels.  which: 0 gemm, 1 ag, 2 rs, 3 moe. */
+int64_t mk_query_workspace_bytes(int32_t which, int64_t M, int64_t N, int64_t K);
+
+/* Number of compute units of the current device (0 if no device). */
+int32_t mk_device_cu_count(void);
+
+const char* mk_last_error_string(void);
+
+/* ABI version, bumped on any signature change. */
+int32_t mk_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* MK_H_ */

@@ -1,0 +1,419 @@
+// mk_capi.hip — the extern "C" boundary of libmk (declared in include/mk.h):
+// argument and shape validation, persistent-grid sizing and role split, and
+// the host-side MoE routing index build.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "../../include/mk.h"
+#include "mk_internal.h"
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_err = buf;
+  return code;
+}
+
+int hip_fail(hipError_t e, const char* where) {
+  g_err = std::string(where) + ": " + hipGetErrorString(e);
+  return (int)e;
+}
+
+struct DevInfo {
+  int cus = 0;
+  bool ok = false;
+};
+
+// Per-device properties, read once per device.
+int device_info(DevInfo* out) {
+  static std::mutex mu;
+  static std::vector<DevInfo> cache;
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+  std::lock_guard<std::mutex> lock(mu);
+  if ((int)cache.size() <= dev) cache.resize(dev + 1);
+  if (!cache[dev].ok) {
+    hipDeviceProp_t prop;
+    e = hipGetDeviceProperties(&prop, dev);
+    if (e != hipSuccess) return hip_fail(e, "hipGetDeviceProperties");
+    if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+      return fail(MK_EDEVICE, "libmk is built for gfx950 only; device %d is %s", dev, prop.gcnArchName);
+    cache[dev].cus = prop.multiProcessorCount;
+    cache[dev].ok = true;
+  }
+  *out = cache[dev];
+  return MK_OK;
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+void fill_common(mk::GemmKParams& p) {
+  std::memset(&p, 0, sizeof p);
+  p.group_m = 8;
+}
+
+// Split `total` workgroups into producers + consumers; enable the XCD remap
+// when both counts are multiples of the 8 XCDs.
+void set_grid(mk::GemmKParams& p, int total, int n_prod, int ntiles) {
+  p.n_prod = n_prod;
+  p.n_cons = std::max(1, std::min(total - n_prod, ntiles));
+  p.xcd_remap = (p.n_cons % 8 == 0 && p.n_prod % 8 == 0) ? 1 : 0;
+}
+
+int check_gemm_shape(int64_t M, int64_t N, int64_t K, int bm) {
+  if (M <= 0 || N <= 0 || K <= 0) return fail(MK_ESHAPE, "M, N, K must be positive (got %lld, %lld, %lld)",
+                                              (long long)M, (long long)N, (long long)K);
+  if (M % bm) return fail(MK_ESHAPE, "M=%lld must be a multiple of %d", (long long)M, bm);
+  if (N % 256) return fail(MK_ESHAPE, "N=%lld must be a multiple of 256", (long long)N);
+  if (K % 64) return fail(MK_ESHAPE, "K=%lld must be a multiple of 64", (long long)K);
+  if (M > (1LL << 30) || N > (1LL << 30) || K > (1LL << 30)) return fail(MK_ESHAPE, "dimension too large");
+  return MK_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* mk_last_error_string(void) { return g_err.c_str(); }
+
+int32_t mk_abi_version(void) { return 1; }
+
+int32_t mk_device_cu_count(void) {
+  DevInfo d;
+  if (device_info(&d) != MK_OK) return 0;
+  return d.cus;
+}
+
+int64_t mk_query_workspace_bytes(int32_t which, int64_t M, int64_t N, int64_t K) {
+  (void)which; (void)M; (void)N; (void)K;
+  return 0;
+}
+
+int mk_gemm(const mk_gemm_args* a, void* stream) {
+  if (!a || !a->A || !a->B || !a->C) return fail(MK_EINVAL, "mk_gemm: null argument");
+  DevInfo d;
+  if (int rc = device_info(&d)) return rc;
+  int bm = a->tile_m;
+  if (bm == 0) {
+    const int64_t t256 = (a->M % 256 == 0) ? (a->M / 256) * (a->N / 256) : 0;
+    bm = (t256 >= d.cus) ? 256 : 128;
+  }
+  if (bm != 128 && bm != 256) return fail(MK_EINVAL, "mk_gemm: tile_m must be 0, 128 or 256");
+  if (int rc = check_gemm_shape(a->M, a->N, a->K, bm)) return rc;
+  if (a->lda < a->K || a->ldb < a->N || a->ldc < a->N || (a->lda | a->ldb | a->ldc) % 8)
+    return fail(MK_ESHAPE, "mk_gemm: leading dimensions must cover the row and be multiples of 8");
+  if (!aligned16(a->A) || !aligned16(a->B) || !aligned16(a->C))
+    return fail(MK_EINVAL, "mk_gemm: pointers must be 16-byte aligned");
+  mk::GemmKParams p;
+  fill_common(p);
+  p.A = static_cast<const uint16_t*>(a->A);
+  p.B = static_cast<const uint16_t*>(a->B);
+  p.C = static_cast<uint16_t*>(a->C);
+  p.lda = a->lda; p.ldb = a->ldb; p.ldc = a->ldc;
+  p.M = (int)a->M; p.N = (int)a->N; p.K = (int)a->K;
+  p.tiles_m = (int)(a->M / bm);
+  p.tiles_n = (int)(a->N / 256);
+  const int total = a->num_cus > 0 ? a->num_cus : d.cus;
+  set_grid(p, total, 0, p.tiles_m * p.tiles_n);
+  hipError_t e = mk::launch_gemm(p, bm, mk::kEpiStore, static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? MK_OK : hip_fail(e, "mk_gemm launch");
+}
+
+int mk_ag_gemm(const mk_ag_gemm_args* a, void* stream) {
+  if (!a || !a->A_full || !a->B || !a->C) return fail(MK_EINVAL, "mk_ag_gemm: null argument");
+  DevInfo d;
+  if (int rc = device_info(&d)) return rc;
+  const int bm = 256;
+  if (int rc = check_gemm_shape(a->M, a->N, a->K, bm)) return rc;
+  const int64_t nflags = a->M / 128;
+  if (a->gated) {
+    if (!a->flags) return fail(MK_EINVAL, "mk_ag_gemm: gated launch needs flags");
+    if (a->epoch == 0) return fail(MK_EINVAL, "mk_ag_gemm: epoch 0 is reserved (flags start at 0)");
+    if (a->stage_order && a->M / bm > mk::kMaxTilesM)
+      return fail(MK_ESHAPE, "mk_ag_gemm: arrival-ordered schedule supports at most %d row tiles", mk::kMaxTilesM);
+    if (nflags + a->M / bm > 8192)
+      return fail(MK_ESHAPE, "mk_ag_gemm: too many flags for the schedule scratch");
+  }
+  if (a->num_producers < 0) return fail(MK_EINVAL, "mk_ag_gemm: num_producers < 0");
+  if (a->gated && a->num_producers > 0 && !a->A_shards)
+    return fail(MK_EINVAL, "mk_ag_gemm: producers need A_shards");
+  const int total = a->num_cus > 0 ? a->num_cus : d.cus;
+  const int n_prod = a->gated ? a->num_producers : 0;
+  if (n_prod >= total) return fail(MK_EINVAL, "mk_ag_gemm: num_producers (%d) leaves no compute workgroups", n_prod);
+  mk::GemmKParams p;
+  fill_common(p);
+  p.A = static_cast<const uint16_t*>(a->A_full);
+  p.B = static_cast<const uint16_t*>(a->B);
+  p.C = static_cast<uint16_t*>(a->C);
+  p.lda = a->K; p.ldb = a->N; p.ldc = a->N;
+  p.M = (int)a->M; p.N = (int)a->N; p.K = (int)a->K;
+  p.tiles_m = (int)(a->M / bm);
+  p.tiles_n = (int)(a->N / 256);
+  set_grid(p, total, n_prod, p.tiles_m * p.tiles_n);
+  p.epoch = a->epoch;
+  p.spin_limit = a->spin_limit;
+  p.err = a->error_word;
+  if (a->gated) {
+    p.a_flags = a->flags;
+    p.a_stage_order = a->stage_order;
+    p.perm_mode = a->stage_order ? mk::kPermArrival : mk::kPermNone;
+    if (n_prod > 0) {
+      p.st_src = static_cast<const uint16_t*>(a->A_shards);
+      p.st_dst = static_cast<uint16_t*>(a->A_full);
+      p.st_cols = (int)a->K;
+      p.st_nblocks = (int)nflags;
+      p.st_order = a->stage_order;
+      p.st_flags = a->flags;
+    }
+  }
+  hipError_t e = mk::launch_gemm(p, bm, mk::kEpiStore, static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? MK_OK : hip_fail(e, "mk_ag_gemm launch");
+}
+
+int mk_gemm_rs(const mk_gemm_rs_args* a, void* stream) {
+  if (!a || !a->A || !a->B || !a->workspace || !a->output) return fail(MK_EINVAL, "mk_gemm_rs: null argument");
+  DevInfo d;
+  if (int rc = device_info(&d)) return rc;
+  const int bm = 256;
+  if (int rc = check_gemm_shape(a->M, a->N, a->K, bm)) return rc;
+  if (a->world < 1 || a->rank < 0 || a->rank >= a->world) return fail(MK_EINVAL, "mk_gemm_rs: bad world/rank");
+  if (a->M % a->world || (a->M / a->world) % bm)
+    return fail(MK_ESHAPE, "mk_gemm_rs: M/world must be a multiple of %d", bm);
+  if (a->M / bm > mk::kMaxTilesM) return fail(MK_ESHAPE, "mk_gemm_rs: at most %d row tiles", mk::kMaxTilesM);
+  const int npeers = a->world - 1;
+  if (npeers > 0 && !a->peer_recv) return fail(MK_EINVAL, "mk_gemm_rs: peer_recv is null");
+  const int own_rows = (int)(a->M / a->world);
+  const int total = a->num_cus > 0 ? a->num_cus : d.cus;
+  const int n_prod = (a->gated && npeers > 0) ? a->num_producers : 0;
+  if (a->gated && npeers > 0) {
+    if (!a->flags) return fail(MK_EINVAL, "mk_gemm_rs: gated launch needs flags");
+    if (a->epoch == 0) return fail(MK_EINVAL, "mk_gemm_rs: epoch 0 is reserved");
+    if (n_prod > 0 && !a->peer_src) return fail(MK_EINVAL, "mk_gemm_rs: producers need peer_src");
+  }
+  if (n_prod < 0 || n_prod >= total) return fail(MK_EINVAL, "mk_gemm_rs: bad num_producers");
+  mk::GemmKParams p;
+  fill_common(p);
+  p.A = static_cast<const uint16_t*>(a->A);
+  p.B = static_cast<const uint16_t*>(a->B);
+  p.C = static_cast<uint16_t*>(a->workspace);
+  p.lda = a->K; p.ldb = a->N; p.ldc = a->N;
+  p.M = (int)a->M; p.N = (int)a->N; p.K = (int)a->K;
+  p.tiles_m = (int)(a->M / bm);
+  p.tiles_n = (int)(a->N / 256);
+  set_grid(p, total, n_prod, p.tiles_m * p.tiles_n);
+  p.perm_mode = mk::kPermOwnedLast;
+  p.rs_own_row0 = a->rank * own_rows;
+  p.rs_own_rows = own_rows;
+  p.rs_npeers = npeers;
+  p.rs_recv = static_cast<const uint16_t*>(a->peer_recv);
+  p.rs_out = static_cast<uint16_t*>(a->output);
+  p.epoch = a->epoch;
+  p.spin_limit = a->spin_limit;
+  p.err = a->error_word;
+  if (a->gated && npeers > 0) {
+    p.rs_flags = a->flags;
+    if (n_prod > 0) {
+      p.st_src = static_cast<const uint16_t*>(a->peer_src);
+      p.st_dst = static_cast<uint16_t*>(a->peer_recv);
+      p.st_cols = (int)a->N;
+      p.st_nblocks = npeers * (own_rows / 128);
+      p.st_order = a->stage_order;
+      p.st_flags = a->flags;
+    }
+  }
+  hipError_t e = mk::launch_gemm(p, bm, mk::kEpiReduce, static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? MK_OK : hip_fail(e, "mk_gemm_rs launch");
+}
+
+// ---------------------------------------------------------------------------
+// MoE
+// ---------------------------------------------------------------------------
+
+int mk_moe_index_sizes(const int32_t* topk_ids, int32_t T, int32_t topk, int32_t e0, int32_t n_local,
+                       int32_t row_block, int64_t* R_out, int64_t* R_pad_out) {
+  if (!topk_ids || !R_out || !R_pad_out) return fail(MK_EINVAL, "mk_moe_index_sizes: null argument");
+  if (T < 0 || topk <= 0 || n_local <= 0 || row_block <= 0 || e0 < 0)
+    return fail(MK_EINVAL, "mk_moe_index_sizes: bad sizes");
+  std::vector<int64_t> cnt(n_local, 0);
+  for (int64_t i = 0; i < (int64_t)T * topk; ++i) {
+    const int e = topk_ids[i] - e0;
+    if (e >= 0 && e < n_local) ++cnt[e];
+  }
+  int64_t R = 0, Rp = 0;
+  for (int e = 0; e < n_local; ++e) {
+    R += cnt[e];
+    Rp += (cnt[e] + row_block - 1) / row_block * row_block;
+  }
+  *R_out = R;
+  *R_pad_out = Rp;
+  return MK_OK;
+}
+
+int mk_moe_build_indices(const int32_t* topk_ids, const float* gates, int32_t T, int32_t topk, int32_t e0,
+                         int32_t n_local, int32_t row_block, const mk_moe_index* o) {
+  if (!topk_ids || !gates || !o) return fail(MK_EINVAL, "mk_moe_build_indices: null argument");
+  int64_t R, Rp;
+  if (int rc = mk_moe_index_sizes(topk_ids, T, topk, e0, n_local, row_block, &R, &Rp)) return rc;
+  // expert_to_tokens: (token, k) pairs per local expert in ascending token
+  // order (reference bench/dispatch_gemm_bench.py:153-160).
+  std::vector<std::vector<std::pair<int32_t, int32_t>>> e2t(n_local);
+  for (int32_t t = 0; t < T; ++t)
+    for (int32_t k = 0; k < topk; ++k) {
+      const int e = topk_ids[(int64_t)t * topk + k] - e0;
+      if (e >= 0 && e < n_local) e2t[e].push_back({t, k});
+    }
+  std::vector<int32_t> owner_count(T, 0);
+  int64_t r = 0;
+  for (int e = 0; e < n_local; ++e) {
+    const int64_t cnt = (int64_t)e2t[e].size();
+    const int64_t padded = (cnt + row_block - 1) / row_block * row_block;
+    if (o->padded_tokens_per_expert) o->padded_tokens_per_expert[e] = (int32_t)padded;
+    if (o->local_rb_per_expert) o->local_rb_per_expert[e] = (int32_t)(cnt / row_block);
+    for (int64_t i = 0; i < padded; ++i, ++r) {
+      const bool real = i < cnt;
+      const int32_t t = real ? e2t[e][i].first : -1;
+      if (o->pull_indices) {
+        o->pull_indices[3 * r + 0] = real ? 0 : -1;
+        o->pull_indices[3 * r + 1] = real ? 0 : -1;
+        o->pull_indices[3 * r + 2] = t;
+      }
+      if (o->row_expert) o->row_expert[r] = e;
+      if (o->rb_expert && (r % row_block) == 0) o->rb_expert[r / row_block] = e;
+      if (o->row_weight) o->row_weight[r] = real ? gates[(int64_t)t * topk + e2t[e][i].second] : 0.f;
+      if (real) ++owner_count[t];
+    }
+  }
+  // Gather CSR (reference bench/dispatch_gemm_glu_combine_bench.py:222-293
+  // with one producer GPU owning every token): slots are handed out in row
+  // order, so token t's contributions occupy owner_offset[t] + 0, 1, ...
+  std::vector<int32_t> off(T + 1, 0);
+  for (int32_t t = 0; t < T; ++t) off[t + 1] = off[t] + owner_count[t];
+  if (o->owner_offset) std::memcpy(o->owner_offset, off.data(), sizeof(int32_t) * (T + 1));
+  std::vector<int32_t> running(T, 0);
+  r = 0;
+  for (int e = 0; e < n_local; ++e) {
+    const int64_t cnt = (int64_t)e2t[e].size();
+    const int64_t padded = (cnt + row_block - 1) / row_block * row_block;
+    for (int64_t i = 0; i < padded; ++i, ++r) {
+      if (i < cnt) {
+        const int32_t t = e2t[e][i].first;
+        const int32_t slot = off[t] + running[t]++;
+        if (o->row_to_slot) o->row_to_slot[r] = slot;
+        if (o->row_to_owner) o->row_to_owner[r] = 0;
+        if (o->slot_to_row) o->slot_to_row[slot] = (int32_t)r;
+      } else {
+        if (o->row_to_slot) o->row_to_slot[r] = 0;
+        if (o->row_to_owner) o->row_to_owner[r] = -1;
+      }
+    }
+  }
+  return MK_OK;
+}
+
+int mk_moe_permute(const mk_moe_permute_args* a, void* stream) {
+  if (!a || !a->tokens || !a->pull_indices || !a->post_tokens) return fail(MK_EINVAL, "mk_moe_permute: null argument");
+  if (a->H <= 0 || a->H % 8) return fail(MK_ESHAPE, "mk_moe_permute: H must be a positive multiple of 8");
+  if (a->R_pad < 0 || a->tokens_per_src <= 0 || a->devs_per_node <= 0) return fail(MK_EINVAL, "mk_moe_permute: bad sizes");
+  DevInfo d;
+  if (int rc = device_info(&d)) return rc;
+  mk::PermuteKParams p{static_cast<const uint16_t*>(a->tokens), a->pull_indices,
+                       static_cast<uint16_t*>(a->post_tokens), a->R_pad, a->H, a->n_src_rows,
+                       a->tokens_per_src, a->devs_per_node};
+  hipError_t e = mk::launch_permute(p, static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? MK_OK : hip_fail(e, "mk_moe_permute launch");
+}
+
+static int grouped_gemm_impl(const void* A, const void* W, void* out, const int32_t* rb_expert,
+                             const int32_t* expert_rows, int64_t R_pad, int64_t K, int64_t Nw, int32_t E,
+                             int32_t mode, int32_t num_cus, hipStream_t stream) {
+  if (!A || !W || !out || (!rb_expert && !expert_rows)) return fail(MK_EINVAL, "mk_moe_grouped_gemm: null argument");
+  if (mode != 0 && mode != 1) return fail(MK_EINVAL, "mk_moe_grouped_gemm: mode must be 0 or 1");
+  if (E <= 0) return fail(MK_EINVAL, "mk_moe_grouped_gemm: num_experts must be positive");
+  if (R_pad == 0) return MK_OK;
+  if (int rc = check_gemm_shape(R_pad, Nw, K, 128)) return rc;
+  DevInfo d;
+  if (int rc = device_info(&d)) return rc;
+  mk::GemmKParams p;
+  fill_common(p);
+  p.A = static_cast<const uint16_t*>(A);
+  p.B = static_cast<const uint16_t*>(W);
+  p.C = static_cast<uint16_t*>(out);
+  p.lda = K; p.ldb = Nw; p.ldc = mode == 1 ? Nw / 2 : Nw;
+  p.b_expert_stride = K * Nw;
+  p.M = (int)R_pad; p.N = (int)Nw; p.K = (int)K;
+  p.tiles_m = (int)(R_pad / 128);
+  p.tiles_n = (int)(Nw / 256);
+  p.rb_expert = rb_expert;
+  p.expert_rows = expert_rows;
+  p.n_experts = E;
+  p.swiglu_I = (int)(Nw / 2);
+  const int total = num_cus > 0 ? num_cus : d.cus;
+  set_grid(p, total, 0, p.tiles_m * p.tiles_n);
+  hipError_t e = mk::launch_gemm(p, 128, mode == 1 ? mk::kEpiSwiGLU : mk::kEpiStore, stream);
+  return e == hipSuccess ? MK_OK : hip_fail(e, "mk_moe_grouped_gemm launch");
+}
+
+int mk_moe_grouped_gemm(const mk_moe_grouped_gemm_args* a, void* stream) {
+  if (!a) return fail(MK_EINVAL, "mk_moe_grouped_gemm: null argument");
+  return grouped_gemm_impl(a->A, a->W, a->out, a->rb_expert, a->padded_tokens_per_expert, a->R_pad, a->K, a->Nw, a->num_experts, a->mode,
+                           a->num_cus, static_cast<hipStream_t>(stream));
+}
+
+int mk_moe_combine(const mk_moe_combine_args* a, void* stream) {
+  if (!a || !a->y_expert || !a->row_weight || !a->owner_offset || !a->y_out)
+    return fail(MK_EINVAL, "mk_moe_combine: null argument");
+  if (a->H <= 0 || a->H % 8) return fail(MK_ESHAPE, "mk_moe_combine: H must be a positive multiple of 8");
+  if (a->out_dtype != 0 && a->out_dtype != 1) return fail(MK_EINVAL, "mk_moe_combine: out_dtype must be 0 or 1");
+  DevInfo d;
+  if (int rc = device_info(&d)) return rc;
+  mk::CombineKParams p{static_cast<const uint16_t*>(a->y_expert), a->row_weight, a->owner_offset, a->slot_to_row,
+                       a->y_out, a->num_tokens, a->H, a->out_dtype};
+  hipError_t e = mk::launch_combine(p, static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? MK_OK : hip_fail(e, "mk_moe_combine launch");
+}
+
+int mk_moe_invert_slots(const int32_t* row_to_slot, const int32_t* row_to_owner, int64_t R_pad,
+                        int32_t* slot_to_row, void* stream) {
+  if (!row_to_slot || !row_to_owner || (!slot_to_row && R_pad > 0))
+    return fail(MK_EINVAL, "mk_moe_invert_slots: null argument");
+  if (R_pad < 0) return fail(MK_EINVAL, "mk_moe_invert_slots: R_pad < 0");
+  DevInfo d;
+  if (int rc = device_info(&d)) return rc;
+  hipError_t e = mk::launch_invert_slots(row_to_slot, row_to_owner, R_pad, slot_to_row, static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? MK_OK : hip_fail(e, "mk_moe_invert_slots launch");
+}
+
+int mk_moe_ffn_combine(const mk_moe_ffn_args* a, void* stream) {
+  if (!a) return fail(MK_EINVAL, "mk_moe_ffn_combine: null argument");
+  if (a->I % 128) return fail(MK_ESHAPE, "mk_moe_ffn_combine: I must be a multiple of 128");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  mk_moe_permute_args pa{a->tokens, a->pull_indices, a->post_tokens, a->R_pad, a->H,
+                         a->n_src_rows, a->tokens_per_src, a->devs_per_node};
+  if (int rc = mk_moe_permute(&pa, stream)) return rc;
+  if (int rc = grouped_gemm_impl(a->post_tokens, a->w1, a->act, a->rb_expert, a->padded_tokens_per_expert, a->R_pad,
+                                 a->H, 2 * a->I, a->num_experts, 1, a->num_cus, s))
+    return rc;
+  if (int rc = grouped_gemm_impl(a->act, a->w2, a->y_expert, a->rb_expert, a->padded_tokens_per_expert, a->R_pad,
+                                 a->I, a->H, a->num_experts, 0, a->num_cus, s))
+    return rc;
+  mk_moe_combine_args ca{a->y_expert, a->row_weight, a->owner_offset, a->slot_to_row, a->y_out,
+                         a->num_tokens, a->H, a->out_dtype};
+  return mk_moe_combine(&ca, stream);
+}
+
+}  // extern "C"

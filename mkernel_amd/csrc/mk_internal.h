@@ -1,0 +1,77 @@
+// mk_internal.h — kernel parameter blocks and launchers shared between the
+// HIP translation units of libmk (not part of the C-ABI).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mk {
+
+enum Epilogue : int { kEpiStore = 0, kEpiSwiGLU = 1, kEpiReduce = 2 };
+enum PermMode : int { kPermNone = 0, kPermArrival = 1, kPermOwnedLast = 2 };
+constexpr int kMaxTilesM = 512;
+
+struct GemmKParams {
+  // operands
+  const uint16_t* A;
+  const uint16_t* B;
+  uint16_t* C;
+  int64_t lda, ldb, ldc;
+  int64_t b_expert_stride;  // elements between experts' B matrices
+  int M, N, K;
+  int tiles_m, tiles_n;
+  int group_m;
+  // grid roles
+  int n_prod, n_cons;
+  int xcd_remap;
+  // grouped GEMM: expert of each BM row tile (nullptr = dense)
+  const int* rb_expert;
+  const int* expert_rows;   // padded rows per expert (used when rb_expert is null)
+  int n_experts;
+  // SwiGLU: width I of the gate half of B's columns
+  int swiglu_I;
+  // consumer A-row gate (AllGather side)
+  const uint32_t* a_flags;
+  const int* a_stage_order;
+  int perm_mode;
+  // reduce epilogue (ReduceScatter side)
+  int rs_own_row0, rs_own_rows, rs_npeers;
+  const uint16_t* rs_recv;
+  uint16_t* rs_out;
+  const uint32_t* rs_flags;
+  // producer staging: block b (128 rows of st_cols) copied st_src -> st_dst
+  const uint16_t* st_src;
+  uint16_t* st_dst;
+  int st_cols, st_nblocks;
+  const int* st_order;
+  uint32_t* st_flags;
+  // flag protocol
+  uint32_t epoch;
+  uint32_t spin_limit;
+  uint32_t* err;
+};
+
+hipError_t launch_gemm(const GemmKParams& p, int bm, int epi, hipStream_t stream);
+
+struct PermuteKParams {
+  const uint16_t* tokens;
+  const int* pull;
+  uint16_t* post;
+  int64_t R_pad, H, n_src_rows;
+  int tokens_per_src, devs_per_node;
+};
+hipError_t launch_permute(const PermuteKParams& p, hipStream_t stream);
+
+struct CombineKParams {
+  const uint16_t* y_expert;
+  const float* row_weight;
+  const int* owner_offset;
+  const int* slot_to_row;
+  void* y_out;
+  int64_t num_tokens, H;
+  int out_dtype;
+};
+hipError_t launch_combine(const CombineKParams& p, hipStream_t stream);
+hipError_t launch_invert_slots(const int* row_to_slot, const int* row_to_owner, int64_t R_pad, int* slot_to_row,
+                               hipStream_t stream);
+
+}  // namespace mk

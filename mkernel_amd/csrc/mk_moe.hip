@@ -1,0 +1,92 @@
+// mk_moe.hip — HBM-bound MoE data movement on gfx950:
+//   * permute: expert-contiguous gather of token rows (reference
+//     src/dispatch_gemm.cu:106-198 dispatch_fused), 128-bit loads/stores;
+//   * combine: deterministic gather of the top-k expert rows of each source
+//     token, weighted and summed in fp32 (reference
+//     src/dispatch_gemm_glu_combine.cu:736-818 combine_gather_owner; the
+//     reference pre-rounds w*y to bf16 in its producer step, here the product
+//     stays fp32 because the rows are read in place on the same GPU).
+#include "mk_device.h"
+#include "mk_internal.h"
+
+namespace mk {
+
+// One workgroup per padded row; padding rows (src_node < 0) are zero-filled.
+__global__ __launch_bounds__(kThreads) void permute_kernel(PermuteKParams p) {
+  const int64_t r = blockIdx.x;
+  const int* pr = p.pull + 3 * r;
+  const int src_node = pr[0], src_dev = pr[1], src_tok = pr[2];
+  const int64_t vec = p.H / 8;
+  uint4* dst = reinterpret_cast<uint4*>(p.post + r * p.H);
+  if (src_node < 0 || src_tok < 0) {
+    const uint4 z = {0u, 0u, 0u, 0u};
+    for (int64_t c = threadIdx.x; c < vec; c += kThreads) dst[c] = z;
+    return;
+  }
+  const int64_t srow = ((int64_t)src_node * p.devs_per_node + src_dev) * p.tokens_per_src + src_tok;
+  const uint4* src = reinterpret_cast<const uint4*>(p.tokens + srow * p.H);
+  for (int64_t c = threadIdx.x; c < vec; c += kThreads) dst[c] = src[c];
+}
+
+hipError_t launch_permute(const PermuteKParams& p, hipStream_t stream) {
+  if (p.R_pad == 0) return hipSuccess;
+  hipLaunchKernelGGL(permute_kernel, dim3((unsigned)p.R_pad), dim3(kThreads), 0, stream, p);
+  return hipGetLastError();
+}
+
+// One workgroup per source token; each thread owns 8 contiguous columns.
+__global__ __launch_bounds__(kThreads) void combine_kernel(CombineKParams p) {
+  const int64_t t = blockIdx.x;
+  const int s0 = p.owner_offset[t], s1 = p.owner_offset[t + 1];
+  const int64_t vec = p.H / 8;
+  for (int64_t c = threadIdx.x; c < vec; c += kThreads) {
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int s = s0; s < s1; ++s) {
+      const int row = p.slot_to_row[s];
+      const float w = p.row_weight[row];
+      const uint4 v = *reinterpret_cast<const uint4*>(p.y_expert + (int64_t)row * p.H + c * 8);
+      acc[0] += w * bf16_lo(v.x);
+      acc[1] += w * bf16_hi(v.x);
+      acc[2] += w * bf16_lo(v.y);
+      acc[3] += w * bf16_hi(v.y);
+      acc[4] += w * bf16_lo(v.z);
+      acc[5] += w * bf16_hi(v.z);
+      acc[6] += w * bf16_lo(v.w);
+      acc[7] += w * bf16_hi(v.w);
+    }
+    if (p.out_dtype == 0) {
+      float4* o = reinterpret_cast<float4*>(static_cast<float*>(p.y_out) + t * p.H + c * 8);
+      o[0] = make_float4(acc[0], acc[1], acc[2], acc[3]);
+      o[1] = make_float4(acc[4], acc[5], acc[6], acc[7]);
+    } else {
+      uint4 w;
+      w.x = pack_bf16x2(acc[0], acc[1]);
+      w.y = pack_bf16x2(acc[2], acc[3]);
+      w.z = pack_bf16x2(acc[4], acc[5]);
+      w.w = pack_bf16x2(acc[6], acc[7]);
+      *reinterpret_cast<uint4*>(static_cast<uint16_t*>(p.y_out) + t * p.H + c * 8) = w;
+    }
+  }
+}
+
+hipError_t launch_combine(const CombineKParams& p, hipStream_t stream) {
+  if (p.num_tokens == 0) return hipSuccess;
+  hipLaunchKernelGGL(combine_kernel, dim3((unsigned)p.num_tokens), dim3(kThreads), 0, stream, p);
+  return hipGetLastError();
+}
+
+__global__ void invert_slots_kernel(const int* row_to_slot, const int* row_to_owner, int64_t R_pad,
+                                    int* slot_to_row) {
+  const int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (r < R_pad && row_to_owner[r] >= 0) slot_to_row[row_to_slot[r]] = (int)r;
+}
+
+hipError_t launch_invert_slots(const int* row_to_slot, const int* row_to_owner, int64_t R_pad, int* slot_to_row,
+                               hipStream_t stream) {
+  if (R_pad == 0) return hipSuccess;
+  hipLaunchKernelGGL(invert_slots_kernel, dim3((unsigned)((R_pad + 255) / 256)), dim3(256), 0, stream, row_to_slot,
+                     row_to_owner, R_pad, slot_to_row);
+  return hipGetLastError();
+}
+
+}  // namespace mk

@@ -1,0 +1,155 @@
+"""Torch-tensor front end of libmk (device memory and streams come from torch;
+every computation runs in libmk's HIP kernels through the C-ABI).
+
+All functions launch on torch's current HIP stream and return immediately.
+Shape/argument problems raise :class:`mkernel_amd.capi.MkError`.
+"""
+from __future__ import annotations
+
+import ctypes as C
+
+import numpy as np
+import torch
+
+from . import capi
+from .capi import (AgGemmArgs, GemmArgs, GemmRsArgs, MoeCombineArgs, MoeFfnArgs, MoeGroupedGemmArgs,
+                   MoeIndex, MoePermuteArgs)
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def _stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _bf16(t: torch.Tensor, name: str) -> None:
+    if t.dtype != torch.bfloat16 or not t.is_cuda or not t.is_contiguous():
+        raise ValueError(f"{name} must be a contiguous bf16 device tensor")
+
+
+def cu_count() -> int:
+    return int(capi.lib().mk_device_cu_count())
+
+
+def gemm(A: torch.Tensor, B: torch.Tensor, out: torch.Tensor | None = None, num_cus: int = 0,
+         tile_m: int = 0) -> torch.Tensor:
+    """C = A @ B (bf16 in, fp32 accumulate, bf16 out)."""
+    _bf16(A, "A"); _bf16(B, "B")
+    M, K = A.shape
+    N = B.shape[1]
+    if out is None:
+        out = torch.empty((M, N), dtype=torch.bfloat16, device=A.device)
+    _bf16(out, "C")
+    capi.call("mk_gemm", GemmArgs(_ptr(A), _ptr(B), _ptr(out), M, N, K, K, N, N, num_cus, tile_m), _stream())
+    return out
+
+
+def ag_gemm(A_shards, A_full, B, C_out, flags, stage_order, epoch: int, gated: bool = True,
+            num_producers: int = 16, num_cus: int = 0, spin_limit: int = 0, error_word=None) -> torch.Tensor:
+    """Flag-gated AllGather+GEMM; see include/mk.h mk_ag_gemm."""
+    _bf16(A_full, "A_full"); _bf16(B, "B"); _bf16(C_out, "C")
+    M, K = A_full.shape
+    N = B.shape[1]
+    args = AgGemmArgs(_ptr(A_shards), _ptr(A_full), _ptr(B), _ptr(C_out), M, N, K, _ptr(flags), _ptr(stage_order),
+                      epoch, int(gated), num_producers, num_cus, spin_limit, _ptr(error_word))
+    capi.call("mk_ag_gemm", args, _stream())
+    return C_out
+
+
+def gemm_rs(A, B, workspace, output, peer_src, peer_recv, world: int, rank: int, flags, stage_order, epoch: int,
+            gated: bool = True, num_producers: int = 16, num_cus: int = 0, spin_limit: int = 0,
+            error_word=None) -> torch.Tensor:
+    """GEMM with the reduce-scatter fold in the epilogue; see mk_gemm_rs."""
+    _bf16(A, "A"); _bf16(B, "B")
+    M, K = A.shape
+    N = B.shape[1]
+    args = GemmRsArgs(_ptr(A), _ptr(B), _ptr(workspace), _ptr(output), _ptr(peer_src), _ptr(peer_recv), M, N, K,
+                      world, rank, _ptr(flags), _ptr(stage_order), epoch, int(gated), num_producers, num_cus,
+                      spin_limit, _ptr(error_word))
+    capi.call("mk_gemm_rs", args, _stream())
+    return output
+
+
+def moe_build_indices(topk_ids: np.ndarray, gates: np.ndarray, e0: int, n_local: int,
+                      row_block: int = capi.ROW_BLOCK) -> dict:
+    """Host-side routing index build (libmk C++); returns numpy arrays."""
+    ids = np.ascontiguousarray(topk_ids, dtype=np.int32)
+    g = np.ascontiguousarray(gates, dtype=np.float32)
+    T, k = ids.shape
+    L = capi.lib()
+    R, Rp = C.c_int64(), C.c_int64()
+    p = lambda a: a.ctypes.data_as(C.c_void_p)
+    capi.check("mk_moe_index_sizes", L.mk_moe_index_sizes(p(ids), T, k, e0, n_local, row_block, C.byref(R), C.byref(Rp)))
+    R, Rp = R.value, Rp.value
+    o = {
+        "padded_tokens_per_expert": np.zeros(n_local, np.int32),
+        "local_rb_per_expert": np.zeros(n_local, np.int32),
+        "pull_indices": np.zeros((Rp, 3), np.int32),
+        "row_expert": np.zeros(Rp, np.int32),
+        "rb_expert": np.zeros(Rp // row_block, np.int32),
+        "row_weight": np.zeros(Rp, np.float32),
+        "owner_offset": np.zeros(T + 1, np.int32),
+        "row_to_slot": np.zeros(Rp, np.int32),
+        "row_to_owner": np.zeros(Rp, np.int32),
+        "slot_to_row": np.zeros(max(R, 1), np.int32),
+    }
+    idx = MoeIndex(*[p(o[f]) for f, _ in MoeIndex._fields_])
+    capi.check("mk_moe_build_indices", L.mk_moe_build_indices(p(ids), p(g), T, k, e0, n_local, row_block, C.byref(idx)))
+    o["slot_to_row"] = o["slot_to_row"][:R]
+    o["R"], o["R_pad"] = R, Rp
+    return o
+
+
+def moe_permute(tokens, pull, post, tokens_per_src: int | None = None, devs_per_node: int = 1):
+    _bf16(tokens, "tokens"); _bf16(post, "post_tokens")
+    R_pad, H = post.shape
+    tps = tokens.shape[0] if tokens_per_src is None else tokens_per_src
+    capi.call("mk_moe_permute", MoePermuteArgs(_ptr(tokens), _ptr(pull), _ptr(post), R_pad, H, tokens.shape[0], tps,
+                                                devs_per_node), _stream())
+    return post
+
+
+def moe_grouped_gemm(A, W, out, rb_expert=None, padded_tokens_per_expert=None, mode: int = 0, num_cus: int = 0):
+    """mode 0: out = A @ W[e]; mode 1: out = silu(h[:, :I]) * h[:, I:], h = A @ W[e]."""
+    _bf16(A, "A"); _bf16(W, "W"); _bf16(out, "out")
+    R_pad, K = A.shape
+    E, _, Nw = W.shape
+    args = MoeGroupedGemmArgs(_ptr(A), _ptr(W), _ptr(out), _ptr(rb_expert), _ptr(padded_tokens_per_expert), R_pad, K,
+                              Nw, E, mode, num_cus)
+    capi.call("mk_moe_grouped_gemm", args, _stream())
+    return out
+
+
+def moe_invert_slots(row_to_slot, row_to_owner, slot_to_row):
+    capi.check("mk_moe_invert_slots", capi.lib().mk_moe_invert_slots(
+        _ptr(row_to_slot), _ptr(row_to_owner), row_to_slot.numel(), _ptr(slot_to_row), C.c_void_p(_stream() or None)))
+    return slot_to_row
+
+
+def moe_combine(y_expert, row_weight, owner_offset, slot_to_row, y_out):
+    _bf16(y_expert, "y_expert")
+    T, H = y_out.shape
+    od = 0 if y_out.dtype == torch.float32 else 1
+    if od == 1 and y_out.dtype != torch.bfloat16:
+        raise ValueError("y_out must be float32 or bfloat16")
+    capi.call("mk_moe_combine", MoeCombineArgs(_ptr(y_expert), _ptr(row_weight), _ptr(owner_offset), _ptr(slot_to_row),
+                                                _ptr(y_out), T, H, od), _stream())
+    return y_out
+
+
+def moe_ffn_combine(tokens, pull, row_weight, owner_offset, slot_to_row, w1, w2, post, act, y_expert, y_out,
+                    rb_expert=None, padded_tokens_per_expert=None, tokens_per_src: int | None = None,
+                    devs_per_node: int = 1, num_cus: int = 0):
+    """permute -> grouped GEMM1 + SwiGLU -> grouped GEMM2 -> combine."""
+    T, H = y_out.shape
+    E, _, I2 = w1.shape
+    R_pad = post.shape[0]
+    od = 0 if y_out.dtype == torch.float32 else 1
+    tps = tokens.shape[0] if tokens_per_src is None else tokens_per_src
+    args = MoeFfnArgs(_ptr(tokens), _ptr(pull), _ptr(rb_expert), _ptr(padded_tokens_per_expert), _ptr(row_weight),
+                      _ptr(owner_offset), _ptr(slot_to_row), _ptr(w1), _ptr(w2), _ptr(post), _ptr(act), _ptr(y_expert),
+                      _ptr(y_out), T, tokens.shape[0], R_pad, H, I2 // 2, E, tps, devs_per_node, od, num_cus)
+    capi.call("mk_moe_ffn_combine", args, _stream())
+    return y_out

@@ -1,0 +1,188 @@
+"""GPU parity of the GEMM core, the flag-gated AllGather consumer and the
+reduce-scatter epilogue against the CPU oracle (all through the C-ABI)."""
+import numpy as np
+import pytest
+import torch
+
+from mkernel_amd import ops, workloads as wl
+from mkernel_amd.capi import MkError
+from oracle.gemm import ag_gemm_ref, gemm_ref, gemm_rs_ref, rel_fro
+
+pytestmark = pytest.mark.gpu
+TOL = 2e-2  # rel-Frobenius bound from BASELINE north_star
+
+
+def _say(msg):
+    print(msg, flush=True)
+
+
+@pytest.mark.parametrize("M,N,K,tile", [(128, 256, 64, 128), (256, 256, 128, 256), (512, 512, 512, 0),
+                                        (384, 768, 1024, 128), (1024, 1280, 320, 256)])
+def test_gemm_vs_oracle(dev, M, N, K, tile):
+    _say(f"gemm M={M} N={N} K={K} tile={tile}")
+    A = wl.randn_bf16((M, K), 10, K ** -0.5)
+    B = wl.randn_bf16((K, N), 11, K ** -0.5)
+    C = ops.gemm(A.to(dev), B.to(dev), tile_m=tile)
+    torch.cuda.synchronize()
+    assert rel_fro(C.float(), gemm_ref(A, B)) < TOL
+    # each output is the fp32 dot product rounded once to bf16
+    ref = gemm_ref(A, B)
+    assert torch.allclose(C.cpu().float(), ref, rtol=2 ** -7, atol=1e-5)
+
+
+@pytest.mark.parametrize("tile", [128, 256])
+def test_gemm_identity_is_exact(dev, tile):
+    """I @ B == B and A @ I == A bit-exactly (pins the operand/accumulator layout)."""
+    _say(f"gemm identity tile={tile}")
+    n = 512
+    I = torch.eye(n, dtype=torch.bfloat16)
+    X = wl.randn_bf16((n, n), 12)
+    assert torch.equal(ops.gemm(I.to(dev), X.to(dev), tile_m=tile).cpu(), X)
+    assert torch.equal(ops.gemm(X.to(dev), I.to(dev), tile_m=tile).cpu(), X)
+
+
+def test_gemm_permutation_exact(dev):
+    """A permutation matrix on the left permutes rows of B exactly."""
+    n = 256
+    perm = torch.randperm(n, generator=torch.Generator().manual_seed(3))
+    P = torch.zeros(n, n, dtype=torch.bfloat16)
+    P[torch.arange(n), perm] = 1
+    X = wl.randn_bf16((n, 512), 13)
+    assert torch.equal(ops.gemm(P.to(dev), X.to(dev)).cpu(), X[perm])
+
+
+def test_gemm_bad_shape_raises(dev):
+    A = torch.zeros((100, 64), dtype=torch.bfloat16, device=dev)
+    B = torch.zeros((64, 256), dtype=torch.bfloat16, device=dev)
+    with pytest.raises(MkError):
+        ops.gemm(A, B)
+
+
+def test_gemm_config1_slice(dev):
+    """Config 1 at full size (4096^3): a 256-row slice against the oracle."""
+    _say("gemm config1 4096^3")
+    A, B = wl.gemm_inputs(wl.GemmCfg(), device="cpu")
+    C = ops.gemm(A.to(dev), B.to(dev))
+    torch.cuda.synchronize()
+    rows = slice(1024, 1280)
+    assert rel_fro(C[rows].float(), gemm_ref(A[rows], B)) < TOL
+    assert torch.isfinite(C.float()).all()
+
+
+def _ag_case(dev, world=8, shard=256, K=512, N=512, seed=0):
+    cfg = wl.AgCfg(world=world, shard_rows=shard, K=K, N=N)
+    A, B, order = wl.ag_inputs(cfg, seed=seed)
+    return cfg, A, B, torch.from_numpy(order)
+
+
+@pytest.mark.parametrize("producers", [1, 4, 16])
+def test_ag_gemm_producer_gated(dev, producers):
+    _say(f"ag_gemm producers={producers}")
+    cfg, A, B, order = _ag_case(dev)
+    Ad, Bd = A.to(dev), B.to(dev)
+    A_full = torch.zeros_like(Ad)
+    flags = torch.zeros(cfg.M // 128, dtype=torch.int32, device=dev)
+    C = torch.empty((cfg.M, cfg.N), dtype=torch.bfloat16, device=dev)
+    ops.ag_gemm(Ad, A_full, Bd, C, flags, order.to(dev), epoch=1, num_producers=producers)
+    torch.cuda.synchronize()
+    assert torch.equal(A_full.cpu(), A)  # staging is a bit-exact copy
+    assert (flags.cpu() == 1).all()
+    ref = ag_gemm_ref(A, B)
+    assert rel_fro(C.float(), ref) < TOL
+    # flag order must not change the result (bit-equal to the ungated GEMM)
+    C2 = torch.empty_like(C)
+    ops.ag_gemm(None, A_full, Bd, C2, None, None, epoch=1, gated=False)
+    torch.cuda.synchronize()
+    assert torch.equal(C.cpu(), C2.cpu())
+
+
+def test_ag_gemm_epochs_and_orders(dev):
+    """Several calls with increasing epochs and different stage orders, no
+    flag reset in between: every result is bit-identical."""
+    cfg, A, B, _ = _ag_case(dev)
+    Ad, Bd = A.to(dev), B.to(dev)
+    flags = torch.zeros(cfg.M // 128, dtype=torch.int32, device=dev)
+    outs = []
+    for epoch, seed in [(1, 5), (2, 6), (3, 7)]:
+        _say(f"ag_gemm epoch={epoch}")
+        A_full = torch.zeros_like(Ad)
+        order = torch.from_numpy(wl.stage_order(cfg.M // 128, seed)).to(dev)
+        C = torch.empty((cfg.M, cfg.N), dtype=torch.bfloat16, device=dev)
+        ops.ag_gemm(Ad, A_full, Bd, C, flags, order, epoch=epoch, num_producers=8)
+        torch.cuda.synchronize()
+        outs.append(C.cpu())
+    assert all(torch.equal(outs[0], o) for o in outs[1:])
+
+
+def test_ag_gemm_preset_flags(dev):
+    """Flags published by someone else (no producer role in the launch)."""
+    cfg, A, B, order = _ag_case(dev)
+    flags = torch.full((cfg.M // 128,), 7, dtype=torch.int32, device=dev)
+    C = torch.empty((cfg.M, cfg.N), dtype=torch.bfloat16, device=dev)
+    ops.ag_gemm(None, A.to(dev), B.to(dev), C, flags, order.to(dev), epoch=7, num_producers=0)
+    torch.cuda.synchronize()
+    assert rel_fro(C.float(), ag_gemm_ref(A, B)) < TOL
+
+
+def test_ag_gemm_bounded_wait_reports_timeout(dev):
+    """A flag nobody publishes: the bounded wait gives up and sets the error
+    word instead of hanging (every wave still exits)."""
+    cfg, A, B, order = _ag_case(dev)
+    flags = torch.zeros(cfg.M // 128, dtype=torch.int32, device=dev)
+    flags[: cfg.M // 256] = 3  # half the tiles published, the rest never
+    err = torch.zeros(1, dtype=torch.int32, device=dev)
+    C = torch.empty((cfg.M, cfg.N), dtype=torch.bfloat16, device=dev)
+    ops.ag_gemm(None, A.to(dev), B.to(dev), C, flags, None, epoch=3, num_producers=0, spin_limit=64,
+                error_word=err)
+    torch.cuda.synchronize()
+    assert int(err.item()) & 1
+    # the published half is still computed correctly
+    half = cfg.M // 2
+    assert rel_fro(C[:half].float(), gemm_ref(A[:half], B)) < TOL
+
+
+@pytest.mark.parametrize("rank,producers", [(0, 4), (3, 8), (7, 0)])
+def test_gemm_rs_vs_oracle(dev, rank, producers):
+    _say(f"gemm_rs rank={rank} producers={producers}")
+    cfg = wl.RsCfg(world=8, rank=rank, M=2048, K=256, N=512)
+    A, B, peers, order = wl.rs_inputs(cfg)
+    rows = cfg.M // cfg.world
+    Ad, Bd = A.to(dev), B.to(dev)
+    work = torch.zeros((cfg.M, cfg.N), dtype=torch.bfloat16, device=dev)
+    out = torch.zeros((rows, cfg.N), dtype=torch.bfloat16, device=dev)
+    nfl = (cfg.world - 1) * rows // 128
+    if producers:
+        recv = torch.zeros_like(peers, device=dev)
+        flags = torch.zeros(nfl, dtype=torch.int32, device=dev)
+    else:
+        recv = peers.to(dev)
+        flags = torch.full((nfl,), 9, dtype=torch.int32, device=dev)
+    ops.gemm_rs(Ad, Bd, work, out, peers.to(dev), recv, cfg.world, rank, flags, torch.from_numpy(order).to(dev),
+                epoch=9, num_producers=producers)
+    torch.cuda.synchronize()
+    P, owned = gemm_rs_ref(A, B, peers, rank, cfg.world)
+    assert rel_fro(out.float(), owned) < TOL
+    mask = torch.ones(cfg.M, dtype=torch.bool)
+    mask[rank * rows:(rank + 1) * rows] = False
+    assert rel_fro(work.cpu()[mask].float(), P[mask]) < TOL
+    assert (work.cpu()[~mask] == 0).all()  # owned rows are not sent
+    if producers:
+        assert torch.equal(recv.cpu(), peers)
+
+
+def test_gemm_rs_equal_partials_known_answer(dev):
+    """All 8 partials equal => output is exactly 8x the partial.  Integer
+    operands in {-1, 0, 1} make every partial an exact small integer."""
+    M, K, N, world, rank = 2048, 128, 256, 8, 2
+    g = torch.Generator().manual_seed(4)
+    A = torch.randint(-1, 2, (M, K), generator=g).to(torch.bfloat16)
+    B = torch.randint(-1, 2, (K, N), generator=g).to(torch.bfloat16)
+    rows = M // world
+    P = (A.float() @ B.float())
+    own = P[rank * rows:(rank + 1) * rows]
+    peers = own.to(torch.bfloat16).unsqueeze(0).repeat(world - 1, 1, 1).contiguous()
+    work = torch.zeros((M, N), dtype=torch.bfloat16, device=dev)
+    out = torch.zeros((rows, N), dtype=torch.bfloat16, device=dev)
+    ops.gemm_rs(A.to(dev), B.to(dev), work, out, None, peers.to(dev), world, rank, None, None, epoch=1, gated=False)
+    torch.cuda.synchronize()
+    assert torch.equal(out.cpu(), (own * world).to(torch.bfloat16))

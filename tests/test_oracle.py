@@ -1,0 +1,164 @@
+"""CPU checks that pin the oracle itself (closed forms, brute force, special
+cases, independent restatements) — no GPU needed."""
+import json
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from mkernel_amd import workloads as wl
+from oracle import gemm as og
+from oracle import moe as om
+from oracle.cmoe import build_indices_c
+
+GOLDEN = Path(__file__).resolve().parent / "golden"
+
+
+# ---------------------------------------------------------------- GEMM ----
+def test_gemm_ref_matches_bruteforce():
+    A = wl.randn_bf16((5, 7), 1)
+    B = wl.randn_bf16((7, 3), 2)
+    assert torch.allclose(og.gemm_ref(A, B).double(), og.gemm_bruteforce(A, B), rtol=1e-6, atol=1e-6)
+
+
+def test_gemm_ref_special_cases():
+    A = wl.randn_bf16((16, 16), 3)
+    I = torch.eye(16, dtype=torch.bfloat16)
+    assert torch.equal(og.gemm_ref(A, I), A.float())
+    assert torch.equal(og.gemm_ref(I, A), A.float())
+    Z = A.clone()
+    Z[4] = 0
+    assert (og.gemm_ref(Z, A)[4] == 0).all()
+    B = wl.randn_bf16((16, 8), 4)
+    assert torch.allclose(og.gemm_ref(A, B).T, og.gemm_ref(B.T.contiguous(), A.T.contiguous()), atol=1e-5)
+
+
+def test_ag_ref_is_gemm_on_gathered_rows():
+    shards = [wl.randn_bf16((4, 8), s) for s in range(3)]
+    B = wl.randn_bf16((8, 5), 9)
+    assert torch.equal(og.ag_gemm_ref(shards, B), og.gemm_ref(torch.cat(shards), B))
+
+
+def test_rs_ref_known_answer():
+    A = wl.randn_bf16((16, 8), 1)
+    B = wl.randn_bf16((8, 4), 2)
+    world, rank = 4, 1
+    P = og.gemm_ref(A, B)
+    own = P[4:8]
+    peers = torch.stack([own] * (world - 1))
+    _, owned = og.gemm_rs_ref(A, B, peers, rank, world)
+    assert torch.allclose(owned, own * world, rtol=1e-6, atol=1e-6)
+    # zero peers => owned slice of the partial
+    _, owned0 = og.gemm_rs_ref(A, B, torch.zeros_like(peers), rank, world)
+    assert torch.equal(owned0, own)
+
+
+def test_rel_fro():
+    x = torch.ones(4, 4)
+    assert og.rel_fro(x, x) == 0.0
+    assert abs(og.rel_fro(1.01 * x, x) - 0.01) < 1e-7
+
+
+# ----------------------------------------------------------------- MoE ----
+def _tiny():
+    return json.loads((GOLDEN / "index_tiny.json").read_text())
+
+
+def test_index_tiny_hand_worked():
+    g = _tiny()
+    out = om.build_indices_py(g["topk_ids"], g["gates"], g["e0"], g["n_local"], g["row_block"])
+    for key, val in g["expected"].items():
+        got = out[key]
+        got = [list(x) for x in got] if key == "pull_indices" else list(got)
+        assert got == val, key
+
+
+@pytest.mark.parametrize("seed,T,E,k,ep,rank", [(0, 64, 16, 4, 4, 0), (1, 300, 64, 8, 8, 3), (2, 1000, 256, 8, 8, 7)])
+def test_index_restatements_agree(seed, T, E, k, ep, rank):
+    ids, gates = wl.zipf_routing(T, E, k, 1.1, seed)
+    n_local = E // ep
+    e0 = rank * n_local
+    rb = 16
+    py = om.build_indices_py(ids, gates, e0, n_local, rb)
+    npv = om.build_indices_np(ids, gates, e0, n_local, rb)
+    cv = build_indices_c(ids, gates, e0, n_local, rb)
+    for key in ("padded_tokens_per_expert", "pull_indices", "row_expert", "row_weight", "owner_offset",
+                "row_to_slot", "row_to_owner", "slot_to_row"):
+        a = np.asarray(py[key])
+        assert np.array_equal(a, np.asarray(npv[key])), key
+        assert np.array_equal(a, np.asarray(cv[key])), key
+    assert np.array_equal(np.asarray(py["rb_expert"]), npv["rb_expert"])
+    assert np.array_equal(np.asarray(py["local_rb_per_expert"]), npv["local_rb_per_expert"])
+
+
+def test_index_invariants():
+    ids, gates = wl.zipf_routing(2048, 256, 8, 1.1, 6)
+    e0, n_local = 64, 32
+    o = om.build_indices_np(ids, gates, e0, n_local)
+    pull = o["pull_indices"]
+    valid = pull[:, 0] >= 0
+    # every local (t, k) appears exactly once
+    local = [(t, j) for t in range(ids.shape[0]) for j in range(8) if e0 <= ids[t, j] < e0 + n_local]
+    assert valid.sum() == len(local) == o["R"]
+    assert sorted(pull[valid, 2].tolist()) == sorted(t for t, _ in local)
+    assert (pull[~valid] == -1).all()
+    assert (o["padded_tokens_per_expert"] % 128 == 0).all()
+    assert o["padded_tokens_per_expert"].sum() == o["R_pad"]
+    # rows of one expert: tokens ascending, padding at the tail
+    start = 0
+    for e, n in enumerate(o["padded_tokens_per_expert"]):
+        seg = pull[start:start + n]
+        toks = seg[seg[:, 0] >= 0, 2]
+        assert (np.diff(toks) > 0).all()
+        assert (o["row_expert"][start:start + n] == e).all()
+        assert (ids[toks] == e0 + e).any(axis=1).all()
+        start += n
+    # CSR: histogram sums to R, slots a permutation, gates carried over
+    assert o["owner_offset"][-1] == o["R"]
+    assert sorted(o["row_to_slot"][valid].tolist()) == list(range(o["R"]))
+    for r in np.nonzero(valid)[0][:200]:
+        t = pull[r, 2]
+        j = list(ids[t]).index(e0 + o["row_expert"][r])
+        assert o["row_weight"][r] == gates[t, j]
+
+
+def test_permute_ref():
+    tok = wl.randn_bf16((10, 8), 1)
+    pull = np.array([[0, 0, 3], [-1, -1, -1], [0, 0, 9]], np.int32)
+    out = om.permute_ref(tok, pull)
+    assert torch.equal(out[0], tok[3]) and torch.equal(out[2], tok[9]) and (out[1] == 0).all()
+
+
+def test_silu_identities():
+    x = torch.linspace(-20, 20, 401)
+    one = torch.ones_like(x)
+    s = om.silu_mul(x, one)
+    assert torch.allclose(s - om.silu_mul(-x, one), x, atol=1e-5)  # odd part
+    assert om.silu_mul(torch.zeros(1), torch.ones(1)).item() == 0.0
+    assert torch.allclose(s[-1], x[-1], rtol=1e-6)  # silu(x) -> x
+    assert abs(s[0].item()) < 1e-6                  # silu(x) -> 0
+    assert torch.allclose(s, torch.nn.functional.silu(x), atol=1e-6)
+
+
+def test_combine_ref_one_hot_and_linearity():
+    T, H = 6, 4
+    ye = wl.randn_bf16((4, H), 3)
+    pull = np.array([[0, 0, 2], [0, 0, 5], [-1, -1, -1], [0, 0, 2]], np.int32)
+    w = np.array([0.5, 2.0, 9.0, 0.25], np.float32)
+    y = om.combine_ref(ye, w, pull, T)
+    assert torch.allclose(y[5], 2.0 * ye[1].float())
+    assert torch.allclose(y[2], 0.5 * ye[0].float() + 0.25 * ye[3].float())
+    assert (y[[0, 1, 3, 4]] == 0).all()
+    y2 = om.combine_ref(ye, 3 * w, pull, T)
+    assert torch.allclose(y2, 3 * y)
+
+
+def test_zipf_routing_properties():
+    ids, gates = wl.zipf_routing(1000, 256, 8, 1.1, 6)
+    assert ids.shape == (1000, 8)
+    assert all(len(set(r)) == 8 for r in ids.tolist())  # distinct experts per token
+    assert np.allclose(gates.sum(1), 1.0, atol=1e-6)
+    assert (np.diff(gates, axis=1) <= 1e-7).all()        # top-k in descending logit order
+    ids2, gates2 = wl.zipf_routing(1000, 256, 8, 1.1, 6)
+    assert np.array_equal(ids, ids2) and np.array_equal(gates, gates2)
