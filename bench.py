@@ -1,0 +1,251 @@
+#!/usr/bin/env python3
+"""Benchmark of libmk's hot path on one MI355X.
+
+Headline workload (the `value`): BASELINE config 2 — one TP=8 rank's share of
+the flag-gated AllGather+GEMM (A_full 16384x8192 assembled from 8 row shards
+by the in-launch producer role, 128-row flags published in a seeded random
+order, B 8192x3584, C 16384x3584, bf16 in / fp32 accumulate / bf16 out).  A
+step is one mk_ag_gemm launch; inputs are resident in HBM before timing.
+
+The same run also reports (under "extra") the ungated GEMM on the same shape
+(the gating overhead), config 1 (4096^3), config 3 (GEMM + reduce-scatter
+epilogue), config 4 (MoE permute + grouped GEMM1) and config 5 (the full MoE
+FFN + combine layer, tokens/s).
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload all|ag|...]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+import numpy as np
+import torch
+
+from mkernel_amd import ops, workloads as wl
+
+METRIC = "fused-GEMM TFLOP/s & % bf16 MFMA peak (1×MI355X); MoE layer tokens/s"
+PEAK_BF16_TFLOPS = 2500.0   # MI355X published dense bf16 MFMA peak
+PEAK_HBM_GBS = 8000.0       # MI355X published HBM3E bandwidth
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+class Timer:
+    """HIP events on torch's current stream — the stream libmk launches on."""
+
+    def __init__(self):
+        self.s = torch.cuda.Event(enable_timing=True)
+        self.e = torch.cuda.Event(enable_timing=True)
+
+    def run(self, fn, steps: int, warmup: int) -> float:
+        for i in range(warmup):
+            fn(i)
+        torch.cuda.synchronize()
+        self.s.record()
+        for i in range(steps):
+            fn(warmup + i)
+        self.e.record()
+        torch.cuda.synchronize()
+        return self.s.elapsed_time(self.e) / steps  # ms per step
+
+
+# --------------------------------------------------------------- workloads
+def bench_ag(steps, warmup, producers, extra):
+    cfg = wl.AgCfg()
+    dev = "cuda"
+    A, B, order = wl.ag_inputs(cfg, device=dev)
+    A_full = torch.zeros_like(A)
+    C = torch.empty((cfg.M, cfg.N), dtype=torch.bfloat16, device=dev)
+    flags = torch.zeros(cfg.M // 128, dtype=torch.int32, device=dev)
+    order_d = torch.from_numpy(order).to(dev)
+    flops = 2.0 * cfg.M * cfg.N * cfg.K
+    t = Timer()
+    # gated with the in-launch producer (each step publishes a new epoch; the
+    # flags are never reset)
+    ms = t.run(lambda i: ops.ag_gemm(A, A_full, B, C, flags, order_d, epoch=i + 1, num_producers=producers),
+               steps, warmup)
+    ms_ungated = t.run(lambda i: ops.ag_gemm(None, A_full, B, C, None, None, epoch=1, gated=False), steps, warmup)
+    # gated, flags already published (pure gating cost, all CUs computing)
+    flags.fill_(10 ** 6)
+    ms_preset = t.run(lambda i: ops.ag_gemm(None, A_full, B, C, flags, order_d, epoch=10 ** 6, num_producers=0),
+                      steps, warmup)
+    extra["ag_gemm"] = {
+        "shape": [cfg.M, cfg.N, cfg.K], "producers": producers,
+        "us_gated_producer": ms * 1e3, "us_ungated": ms_ungated * 1e3, "us_gated_flags_preset": ms_preset * 1e3,
+        "tflops_gated_producer": flops / ms / 1e9, "tflops_ungated": flops / ms_ungated / 1e9,
+        "gating_overhead_producer": ms / ms_ungated - 1.0, "gating_overhead_flag_check": ms_preset / ms_ungated - 1.0,
+        "staging_bytes": 2 * A.numel() * 2,
+    }
+    return ms, flops, (A_full, B)
+
+
+def bench_gemm(steps, warmup, extra):
+    cfg = wl.GemmCfg()
+    A, B = wl.gemm_inputs(cfg, device="cuda")
+    C = torch.empty((cfg.M, cfg.N), dtype=torch.bfloat16, device="cuda")
+    flops = 2.0 * cfg.M * cfg.N * cfg.K
+    ms = Timer().run(lambda i: ops.gemm(A, B, C), steps, warmup)
+    extra["gemm_4096"] = {"us": ms * 1e3, "tflops": flops / ms / 1e9, "frac_peak": flops / ms / 1e9 / PEAK_BF16_TFLOPS}
+
+
+def bench_rs(steps, warmup, producers, extra):
+    cfg = wl.RsCfg()
+    A, B, peers, order = wl.rs_inputs(cfg, device="cuda")
+    rows = cfg.M // cfg.world
+    work = torch.empty((cfg.M, cfg.N), dtype=torch.bfloat16, device="cuda")
+    out = torch.empty((rows, cfg.N), dtype=torch.bfloat16, device="cuda")
+    recv = torch.empty_like(peers)
+    flags = torch.zeros((cfg.world - 1) * rows // 128, dtype=torch.int32, device="cuda")
+    order_d = torch.from_numpy(order).to("cuda")
+    flops = 2.0 * cfg.M * cfg.N * cfg.K
+    t = Timer()
+    ms = t.run(lambda i: ops.gemm_rs(A, B, work, out, peers, recv, cfg.world, cfg.rank, flags, order_d, epoch=i + 1,
+                                     num_producers=producers), steps, warmup)
+    ms_plain = t.run(lambda i: ops.gemm(A, B, work), steps, warmup)
+    extra["gemm_rs"] = {"shape": [cfg.M, cfg.N, cfg.K], "producers": producers, "us": ms * 1e3,
+                        "tflops": flops / ms / 1e9, "us_plain_gemm_same_shape": ms_plain * 1e3,
+                        "epilogue_bytes_read": peers.numel() * 2}
+
+
+def moe_setup(cfg: wl.MoeCfg):
+    tokens, ids, gates, w1, w2 = wl.moe_inputs(cfg, device="cuda")
+    idx = ops.moe_build_indices(ids, gates, cfg.e0, cfg.n_local)
+    d = {k: torch.from_numpy(np.ascontiguousarray(v)).cuda() for k, v in idx.items() if isinstance(v, np.ndarray)}
+    return tokens, w1, w2, idx, d
+
+
+def bench_moe(steps, warmup, extra):
+    cfg = wl.MoeCfg()
+    tokens, w1, w2, idx, d = moe_setup(cfg)
+    R, R_pad = idx["R"], idx["R_pad"]
+    post = torch.empty((R_pad, cfg.H), dtype=torch.bfloat16, device="cuda")
+    h = torch.empty((R_pad, 2 * cfg.I), dtype=torch.bfloat16, device="cuda")
+    act = torch.empty((R_pad, cfg.I), dtype=torch.bfloat16, device="cuda")
+    ye = torch.empty((R_pad, cfg.H), dtype=torch.bfloat16, device="cuda")
+    y = torch.empty((cfg.tokens, cfg.H), dtype=torch.bfloat16, device="cuda")
+    t = Timer()
+
+    def dispatch_gemm(i):
+        ops.moe_permute(tokens, d["pull_indices"], post)
+        ops.moe_grouped_gemm(post, w1, h, rb_expert=d["rb_expert"], mode=0)
+
+    ms4 = t.run(dispatch_gemm, steps, warmup)
+    ms_perm = t.run(lambda i: ops.moe_permute(tokens, d["pull_indices"], post), steps, warmup)
+    ms_g1 = t.run(lambda i: ops.moe_grouped_gemm(post, w1, act, rb_expert=d["rb_expert"], mode=1), steps, warmup)
+    ms_g2 = t.run(lambda i: ops.moe_grouped_gemm(act, w2, ye, rb_expert=d["rb_expert"], mode=0), steps, warmup)
+    ms_comb = t.run(lambda i: ops.moe_combine(ye, d["row_weight"], d["owner_offset"], d["slot_to_row"], y),
+                    steps, warmup)
+    ms5 = t.run(lambda i: ops.moe_ffn_combine(tokens, d["pull_indices"], d["row_weight"], d["owner_offset"],
+                                              d["slot_to_row"], w1, w2, post, act, ye, y, rb_expert=d["rb_expert"]),
+                steps, warmup)
+    used = idx["padded_tokens_per_expert"] > 0
+    w_bytes1 = int(used.sum()) * cfg.H * 2 * cfg.I * 2
+    w_bytes2 = int(used.sum()) * cfg.I * cfg.H * 2
+    f4 = 2.0 * R * cfg.H * 2 * cfg.I
+    f5 = 6.0 * R * cfg.H * cfg.I
+    layer_bytes = w_bytes1 + w_bytes2 + 2 * R_pad * cfg.H * 2 * 2 + R_pad * cfg.I * 2 * 2 + cfg.tokens * cfg.H * 4
+    extra["moe_dispatch_gemm1"] = {"R": R, "R_pad": R_pad, "experts_used": int(used.sum()), "us": ms4 * 1e3,
+                                   "tflops": f4 / ms4 / 1e9, "us_permute": ms_perm * 1e3,
+                                   "permute_GBs": 2 * R_pad * cfg.H * 2 / ms_perm / 1e6}
+    extra["moe_ffn_combine"] = {"us": ms5 * 1e3, "tokens_per_s": cfg.tokens / ms5 * 1e3, "tflops": f5 / ms5 / 1e9,
+                                "frac_peak": f5 / ms5 / 1e9 / PEAK_BF16_TFLOPS,
+                                "hbm_bound_GBs": layer_bytes / ms5 / 1e6,
+                                "us_gemm1_swiglu": ms_g1 * 1e3, "us_gemm2": ms_g2 * 1e3, "us_combine": ms_comb * 1e3,
+                                "weight_bytes": w_bytes1 + w_bytes2}
+
+
+# ------------------------------------------------------------ CPU baseline
+def cpu_baseline(A_full, B, rows: int = 256, reps: int = 3):
+    """The oracle's float32 torch matmul on the host cores, on a bounded
+    sample of the same workload: `rows` rows of A_full times B."""
+    from oracle.gemm import gemm_ref  # CPU baseline leg only
+    torch.set_num_threads(os.cpu_count() or 1)
+    a = A_full[:rows].cpu()
+    b = B.cpu()
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        gemm_ref(a, b)
+        times.append(time.perf_counter() - t0)
+    t = statistics.median(times)
+    flops = 2.0 * rows * b.shape[0] * b.shape[1]
+    return {"value": flops / t / 1e12, "unit": "TFLOP/s", "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"A_full[:{rows}] @ B ({rows}x{b.shape[0]}x{b.shape[1]}, fp32 torch on CPU), median of {reps}"}
+
+
+def load_traffic():
+    """HBM bytes per launch measured with rocprofv3 --pmc (FETCH_SIZE +
+    WRITE_SIZE, scaled by the copy-kernel calibration), if recorded."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            return json.load(f).get("ag_gemm_gated_bytes_per_launch")
+    except (OSError, ValueError):
+        return None
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--producers", type=int, default=16)
+    ap.add_argument("--workload", default="all", choices=["all", "ag", "gemm", "rs", "moe"])
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU's share of the path; runs on more than one GPU are not part of this "
+              "build (see DESIGN.md for how the path shards)", file=sys.stderr)
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print("bench.py needs an MI355X GPU", file=sys.stderr)
+        sys.exit(1)
+    torch.cuda.set_device(0)
+    extra = {}
+    W, K = args.warmup, args.steps
+    line = None
+    if args.workload in ("all", "ag"):
+        log("[bench] ag_gemm config 2")
+        ms, flops, (A_full, B) = bench_ag(K, W, args.producers, extra)
+        tflops = flops / ms / 1e9
+        line = {
+            "metric": METRIC, "value": round(tflops, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": K, "warmup": W,
+            "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+            "dtype": "bf16", "data": "synthetic (seeded N(0,1)/sqrt(K) bf16; seeded random stage order)",
+            "config": {"workload": "ag_gemm: one TP=8 rank's share, A_full 16384x8192 (8 staged shards), "
+                                   "B 8192x3584, C 16384x3584, 128-row flags, in-launch producer role",
+                       "M": 16384, "N": 3584, "K": 8192, "producers": args.producers, "parallelism": "tp8-rank-share"},
+            "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                         "frac": round(tflops / PEAK_BF16_TFLOPS, 4), "traffic": load_traffic()},
+        }
+        if not args.no_cpu:
+            log("[bench] cpu baseline")
+            line["cpu_baseline"] = cpu_baseline(A_full, B)
+        del A_full, B
+        torch.cuda.empty_cache()
+    if args.workload in ("all", "gemm"):
+        log("[bench] gemm config 1")
+        bench_gemm(K, W, extra)
+    if args.workload in ("all", "rs"):
+        log("[bench] gemm_rs config 3")
+        bench_rs(K, W, args.producers, extra)
+        torch.cuda.empty_cache()
+    if args.workload in ("all", "moe"):
+        log("[bench] moe configs 4/5")
+        bench_moe(K, W, extra)
+    if line is None:
+        line = {"metric": METRIC, "value": None, "unit": "TFLOP/s", "n_gpus": 1, "steps": K, "warmup": W}
+    line["extra"] = {k: {kk: (round(vv, 4) if isinstance(vv, float) else vv) for kk, vv in v.items()}
+                     for k, v in extra.items()}
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

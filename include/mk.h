@@ -37,7 +37,7 @@ extern "C" {
  * Replaces the compute role shared by ag_gemm / gemm_rs
  * (reference src/gemm_rs.cu:36-114 compute_tile_impl,
  *  src/ag_gemm.cu:265-461 fused_comp_sm).
- * Requires M % 128 == 0, N % 256 == 0, K % 64 == 0, ld* >= row width and
+ * Requires M % 128 == 0, N % 256 == 0, K % 32 == 0, ld* >= row width and
  * ld* % 8 == 0. */
 typedef struct mk_gemm_args {
   const void* A;  /* bf16 [M, lda] */
@@ -47,6 +47,7 @@ typedef struct mk_gemm_args {
   int64_t lda, ldb, ldc;
   int32_t num_cus; /* persistent grid size; 0 = every CU of the device */
   int32_t tile_m;  /* 0 = auto, else 128 or 256 */
+  int32_t waves;   /* waves per workgroup: 0 = auto, 4 (one per SIMD) or 8 (two per SIMD) */
 } mk_gemm_args;
 int mk_gemm(const mk_gemm_args* args, void* stream);
 

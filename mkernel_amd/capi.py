@@ -47,7 +47,8 @@ class MkError(RuntimeError):
 
 class GemmArgs(C.Structure):
     _fields_ = [("A", vp), ("B", vp), ("C", vp), ("M", i64), ("N", i64), ("K", i64),
-                ("lda", i64), ("ldb", i64), ("ldc", i64), ("num_cus", i32), ("tile_m", i32)]
+                ("lda", i64), ("ldb", i64), ("ldc", i64), ("num_cus", i32), ("tile_m", i32),
+                ("waves", i32)]
 
 
 class AgGemmArgs(C.Structure):

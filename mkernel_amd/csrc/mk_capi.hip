@@ -65,6 +65,7 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 void fill_common(mk::GemmKParams& p) {
   std::memset(&p, 0, sizeof p);
   p.group_m = 8;
+  p.waves = 8;
 }
 
 // Split `total` workgroups into producers + consumers; enable the XCD remap
@@ -80,7 +81,7 @@ int check_gemm_shape(int64_t M, int64_t N, int64_t K, int bm) {
                                               (long long)M, (long long)N, (long long)K);
   if (M % bm) return fail(MK_ESHAPE, "M=%lld must be a multiple of %d", (long long)M, bm);
   if (N % 256) return fail(MK_ESHAPE, "N=%lld must be a multiple of 256", (long long)N);
-  if (K % 64) return fail(MK_ESHAPE, "K=%lld must be a multiple of 64", (long long)K);
+  if (K % 32) return fail(MK_ESHAPE, "K=%lld must be a multiple of 32", (long long)K);
   if (M > (1LL << 30) || N > (1LL << 30) || K > (1LL << 30)) return fail(MK_ESHAPE, "dimension too large");
   return MK_OK;
 }
@@ -114,6 +115,7 @@ int mk_gemm(const mk_gemm_args* a, void* stream) {
     bm = (t256 >= d.cus) ? 256 : 128;
   }
   if (bm != 128 && bm != 256) return fail(MK_EINVAL, "mk_gemm: tile_m must be 0, 128 or 256");
+  if (a->waves != 0 && a->waves != 4 && a->waves != 8) return fail(MK_EINVAL, "mk_gemm: waves must be 0, 4 or 8");
   if (int rc = check_gemm_shape(a->M, a->N, a->K, bm)) return rc;
   if (a->lda < a->K || a->ldb < a->N || a->ldc < a->N || (a->lda | a->ldb | a->ldc) % 8)
     return fail(MK_ESHAPE, "mk_gemm: leading dimensions must cover the row and be multiples of 8");
@@ -130,6 +132,7 @@ int mk_gemm(const mk_gemm_args* a, void* stream) {
   p.tiles_n = (int)(a->N / 256);
   const int total = a->num_cus > 0 ? a->num_cus : d.cus;
   set_grid(p, total, 0, p.tiles_m * p.tiles_n);
+  if (a->waves) p.waves = a->waves;
   hipError_t e = mk::launch_gemm(p, bm, mk::kEpiStore, static_cast<hipStream_t>(stream));
   return e == hipSuccess ? MK_OK : hip_fail(e, "mk_gemm launch");
 }

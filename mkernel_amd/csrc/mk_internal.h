@@ -23,6 +23,7 @@ struct GemmKParams {
   // grid roles
   int n_prod, n_cons;
   int xcd_remap;
+  int waves;                // 4 (one wave per SIMD) or 8 (two per SIMD)
   // grouped GEMM: expert of each BM row tile (nullptr = dense)
   const int* rb_expert;
   const int* expert_rows;   // padded rows per expert (used when rb_expert is null)

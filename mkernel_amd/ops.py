@@ -34,7 +34,7 @@ def cu_count() -> int:
 
 
 def gemm(A: torch.Tensor, B: torch.Tensor, out: torch.Tensor | None = None, num_cus: int = 0,
-         tile_m: int = 0) -> torch.Tensor:
+         tile_m: int = 0, waves: int = 0) -> torch.Tensor:
     """C = A @ B (bf16 in, fp32 accumulate, bf16 out)."""
     _bf16(A, "A"); _bf16(B, "B")
     M, K = A.shape
@@ -42,7 +42,7 @@ def gemm(A: torch.Tensor, B: torch.Tensor, out: torch.Tensor | None = None, num_
     if out is None:
         out = torch.empty((M, N), dtype=torch.bfloat16, device=A.device)
     _bf16(out, "C")
-    capi.call("mk_gemm", GemmArgs(_ptr(A), _ptr(B), _ptr(out), M, N, K, K, N, N, num_cus, tile_m), _stream())
+    capi.call("mk_gemm", GemmArgs(_ptr(A), _ptr(B), _ptr(out), M, N, K, K, N, N, num_cus, tile_m, waves), _stream())
     return out
 
 

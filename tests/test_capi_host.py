@@ -30,7 +30,7 @@ def test_library_exports_every_declared_symbol():
     assert L.mk_abi_version() == 1
 
 
-@pytest.mark.parametrize("cls,nfields", [(capi.GemmArgs, 11), (capi.AgGemmArgs, 15), (capi.GemmRsArgs, 19),
+@pytest.mark.parametrize("cls,nfields", [(capi.GemmArgs, 12), (capi.AgGemmArgs, 15), (capi.GemmRsArgs, 19),
                                          (capi.MoeIndex, 10), (capi.MoeGroupedGemmArgs, 11)])
 def test_struct_layouts(cls, nfields):
     assert len(cls._fields_) == nfields

@@ -16,13 +16,15 @@ def _say(msg):
     print(msg, flush=True)
 
 
+@pytest.mark.parametrize("waves", [4, 8])
 @pytest.mark.parametrize("M,N,K,tile", [(128, 256, 64, 128), (256, 256, 128, 256), (512, 512, 512, 0),
-                                        (384, 768, 1024, 128), (1024, 1280, 320, 256)])
-def test_gemm_vs_oracle(dev, M, N, K, tile):
-    _say(f"gemm M={M} N={N} K={K} tile={tile}")
+                                        (384, 768, 1024, 128), (1024, 1280, 320, 256), (256, 512, 32, 256),
+                                        (128, 256, 96, 128)])
+def test_gemm_vs_oracle(dev, M, N, K, tile, waves):
+    _say(f"gemm M={M} N={N} K={K} tile={tile} waves={waves}")
     A = wl.randn_bf16((M, K), 10, K ** -0.5)
     B = wl.randn_bf16((K, N), 11, K ** -0.5)
-    C = ops.gemm(A.to(dev), B.to(dev), tile_m=tile)
+    C = ops.gemm(A.to(dev), B.to(dev), tile_m=tile, waves=waves)
     torch.cuda.synchronize()
     assert rel_fro(C.float(), gemm_ref(A, B)) < TOL
     # each output is the fp32 dot product rounded once to bf16
@@ -30,15 +32,16 @@ def test_gemm_vs_oracle(dev, M, N, K, tile):
     assert torch.allclose(C.cpu().float(), ref, rtol=2 ** -7, atol=1e-5)
 
 
+@pytest.mark.parametrize("waves", [4, 8])
 @pytest.mark.parametrize("tile", [128, 256])
-def test_gemm_identity_is_exact(dev, tile):
+def test_gemm_identity_is_exact(dev, tile, waves):
     """I @ B == B and A @ I == A bit-exactly (pins the operand/accumulator layout)."""
-    _say(f"gemm identity tile={tile}")
+    _say(f"gemm identity tile={tile} waves={waves}")
     n = 512
     I = torch.eye(n, dtype=torch.bfloat16)
     X = wl.randn_bf16((n, n), 12)
-    assert torch.equal(ops.gemm(I.to(dev), X.to(dev), tile_m=tile).cpu(), X)
-    assert torch.equal(ops.gemm(X.to(dev), I.to(dev), tile_m=tile).cpu(), X)
+    assert torch.equal(ops.gemm(I.to(dev), X.to(dev), tile_m=tile, waves=waves).cpu(), X)
+    assert torch.equal(ops.gemm(X.to(dev), I.to(dev), tile_m=tile, waves=waves).cpu(), X)
 
 
 def test_gemm_permutation_exact(dev):
