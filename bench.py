@@ -196,7 +196,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--producers", type=int, default=16)
+    ap.add_argument("--producers", type=int, default=32)
     ap.add_argument("--workload", default="all", choices=["all", "ag", "gemm", "rs", "moe"])
     ap.add_argument("--no-cpu", action="store_true")
     args = ap.parse_args()

@@ -61,8 +61,12 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
 __device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 
-// Wait until *flag has reached `epoch` (wrap-safe).  Returns false (and sets
-// bit 0 of *err) after `limit` polls when limit != 0.
+// Wait until *flag has reached `epoch` (wrap-safe).  Polls are relaxed
+// agent-scope loads spaced by s_sleep with a growing interval (64 .. 1024
+// cycles), so a few hundred waiting workgroups do not flood the L2 the
+// producers are writing through; one acquire fence follows the successful
+// poll.  Returns false (and sets bit 0 of *err) after `limit` polls when
+// limit != 0.
 __device__ __forceinline__ bool wait_flag(const uint32_t* flag, uint32_t epoch, uint32_t limit,
                                           uint32_t* err) {
   uint32_t polls = 0;
@@ -73,7 +77,10 @@ __device__ __forceinline__ bool wait_flag(const uint32_t* flag, uint32_t epoch, 
       if (err) __hip_atomic_fetch_or(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       return false;
     }
-    __builtin_amdgcn_s_sleep(2);
+    if (polls < 8) __builtin_amdgcn_s_sleep(1);
+    else if (polls < 64) __builtin_amdgcn_s_sleep(4);
+    else __builtin_amdgcn_s_sleep(16);
+    if (limit == 0) ++polls;
   }
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
   return true;

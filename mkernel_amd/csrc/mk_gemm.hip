@@ -98,21 +98,23 @@ __device__ __forceinline__ int b_col(const GemmKParams& p, int tn, int q) {
 template <int NT>
 __device__ void producer_role(const GemmKParams& p, int pid) {
   const int64_t block_elems = (int64_t)kFlagRows * p.st_cols;
-  const int64_t block_vec = block_elems / 8;  // uint4 units
+  const int64_t block_vec = block_elems / 8;  // 16-byte units
   constexpr int U = 16;                       // 16-byte loads in flight per thread
   for (int i = pid; i < p.st_nblocks; i += p.n_prod) {
     const int b = p.st_order ? p.st_order[i] : i;
-    const uint4* src = reinterpret_cast<const uint4*>(p.st_src + (int64_t)b * block_elems);
-    uint4* dst = reinterpret_cast<uint4*>(p.st_dst + (int64_t)b * block_elems);
+    // Streaming copy: nontemporal loads and stores keep the staged bytes
+    // out of the caches the compute role is using.
+    const u32x4_t* src = reinterpret_cast<const u32x4_t*>(p.st_src + (int64_t)b * block_elems);
+    u32x4_t* dst = reinterpret_cast<u32x4_t*>(p.st_dst + (int64_t)b * block_elems);
     int64_t base = threadIdx.x;
     for (; base + (int64_t)(U - 1) * NT < block_vec; base += (int64_t)U * NT) {
-      uint4 v[U];
+      u32x4_t v[U];
 #pragma unroll
-      for (int u = 0; u < U; ++u) v[u] = src[base + u * NT];
+      for (int u = 0; u < U; ++u) v[u] = __builtin_nontemporal_load(src + base + u * NT);
 #pragma unroll
-      for (int u = 0; u < U; ++u) dst[base + u * NT] = v[u];
+      for (int u = 0; u < U; ++u) __builtin_nontemporal_store(v[u], dst + base + u * NT);
     }
-    for (; base < block_vec; base += NT) dst[base] = src[base];
+    for (; base < block_vec; base += NT) __builtin_nontemporal_store(__builtin_nontemporal_load(src + base), dst + base);
     __threadfence();
     __syncthreads();
     if (threadIdx.x == 0) publish_flag(p.st_flags + b, p.epoch);
@@ -190,8 +192,9 @@ __device__ __forceinline__ void store_tile(const GemmKParams& p, f32x16 (&acc)[C
       if (p.rs_flags) {
         const int rbs = p.rs_own_rows / kFlagRows;
         constexpr int per = C::BM / kFlagRows;
-        if (tid < p.rs_npeers * per)
-          wait_flag(p.rs_flags + (tid / per) * rbs + lr0 / kFlagRows + tid % per, p.epoch, p.spin_limit, p.err);
+        if (tid == 0)
+          for (int f = 0; f < p.rs_npeers * per; ++f)
+            wait_flag(p.rs_flags + (f / per) * rbs + lr0 / kFlagRows + f % per, p.epoch, p.spin_limit, p.err);
         __syncthreads();
       }
       const int64_t peer_stride = (int64_t)p.rs_own_rows * p.ldc;
@@ -336,7 +339,8 @@ __device__ void compute_role(const GemmKParams& p, int cons_id, char* smem, cons
 
     // Flag gate on the A rows of this tile (AllGather consumer side).
     if (p.a_flags) {
-      if (tid < C::BM / kFlagRows) wait_flag(p.a_flags + (m0 / kFlagRows) + tid, p.epoch, p.spin_limit, p.err);
+      if (tid == 0)
+        for (int f = 0; f < C::BM / kFlagRows; ++f) wait_flag(p.a_flags + m0 / kFlagRows + f, p.epoch, p.spin_limit, p.err);
       __syncthreads();
     }
 

@@ -47,7 +47,7 @@ def gemm(A: torch.Tensor, B: torch.Tensor, out: torch.Tensor | None = None, num_
 
 
 def ag_gemm(A_shards, A_full, B, C_out, flags, stage_order, epoch: int, gated: bool = True,
-            num_producers: int = 16, num_cus: int = 0, spin_limit: int = 0, error_word=None) -> torch.Tensor:
+            num_producers: int = 32, num_cus: int = 0, spin_limit: int = 0, error_word=None) -> torch.Tensor:
     """Flag-gated AllGather+GEMM; see include/mk.h mk_ag_gemm."""
     _bf16(A_full, "A_full"); _bf16(B, "B"); _bf16(C_out, "C")
     M, K = A_full.shape
