@@ -197,7 +197,7 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--producers", type=int, default=32)
-    ap.add_argument("--workload", default="all", choices=["all", "ag", "gemm", "rs", "moe"])
+    ap.add_argument("--workload", default="all", choices=["all", "ag", "gemm", "rs", "moe", "calib"])
     ap.add_argument("--no-cpu", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -240,6 +240,17 @@ def main():
     if args.workload in ("all", "moe"):
         log("[bench] moe configs 4/5")
         bench_moe(K, W, extra)
+    if args.workload == "calib":
+        # HBM-counter calibration: libmk's permute kernel as a plain copy of
+        # a known size (identity row map, 256 MiB read + 256 MiB written).
+        rows, H = 16384, 8192
+        src = torch.ones((rows, H), dtype=torch.bfloat16, device="cuda")
+        dst = torch.empty_like(src)
+        pull = torch.zeros((rows, 3), dtype=torch.int32, device="cuda")
+        pull[:, 2] = torch.arange(rows, dtype=torch.int32, device="cuda")
+        ms = Timer().run(lambda i: ops.moe_permute(src, pull, dst), K, W)
+        extra["copy_calibration"] = {"bytes_read": rows * H * 2, "bytes_written": rows * H * 2, "us": ms * 1e3,
+                                     "GBs": 2 * rows * H * 2 / ms / 1e6}
     if line is None:
         line = {"metric": METRIC, "value": None, "unit": "TFLOP/s", "n_gpus": 1, "steps": K, "warmup": W}
     line["extra"] = {k: {kk: (round(vv, 4) if isinstance(vv, float) else vv) for kk, vv in v.items()}
