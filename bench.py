@@ -56,6 +56,18 @@ class Timer:
         return self.s.elapsed_time(self.e) / steps  # ms per step
 
 
+def interleaved(variants: dict, steps: int, warmup: int, rounds: int = 3) -> dict:
+    """Time several variants of one workload in alternating rounds (the GPU's
+    clock and power state drift over a run, so back-to-back blocks of one
+    variant bias the comparison); returns the median ms per step of each."""
+    t = Timer()
+    res = {k: [] for k in variants}
+    for r in range(rounds):
+        for k, fn in variants.items():
+            res[k].append(t.run(fn, steps, warmup if r == 0 else 1))
+    return {k: statistics.median(v) for k, v in res.items()}
+
+
 # --------------------------------------------------------------- workloads
 def bench_ag(steps, warmup, producers, extra):
     cfg = wl.AgCfg()
@@ -64,21 +76,29 @@ def bench_ag(steps, warmup, producers, extra):
     A_full = torch.zeros_like(A)
     C = torch.empty((cfg.M, cfg.N), dtype=torch.bfloat16, device=dev)
     flags = torch.zeros(cfg.M // 128, dtype=torch.int32, device=dev)
+    counters = torch.zeros(cfg.M // 128, dtype=torch.int32, device=dev)
     order_d = torch.from_numpy(order).to(dev)
     flops = 2.0 * cfg.M * cfg.N * cfg.K
-    t = Timer()
-    # gated with the in-launch producer (each step publishes a new epoch; the
-    # flags are never reset)
-    ms = t.run(lambda i: ops.ag_gemm(A, A_full, B, C, flags, order_d, epoch=i + 1, num_producers=producers),
-               steps, warmup)
-    ms_ungated = t.run(lambda i: ops.ag_gemm(None, A_full, B, C, None, None, epoch=1, gated=False), steps, warmup)
-    # gated, flags already published (pure gating cost, all CUs computing)
-    flags.fill_(10 ** 6)
-    ms_preset = t.run(lambda i: ops.ag_gemm(None, A_full, B, C, flags, order_d, epoch=10 ** 6, num_producers=0),
-                      steps, warmup)
+    epoch = [0]
+
+    def gated(i, prod):
+        # every step publishes a new epoch; flags and counters are never reset
+        epoch[0] += 1
+        ops.ag_gemm(A, A_full, B, C, flags, order_d, epoch=epoch[0], num_producers=prod, stage_counters=counters)
+
+    flags_pub = torch.full_like(flags, 2 ** 30)
+    r = interleaved({
+        "gated": lambda i: gated(i, producers),
+        "dedicated": lambda i: gated(i, 32),
+        "ungated": lambda i: ops.ag_gemm(None, A_full, B, C, None, None, epoch=1, gated=False, num_producers=0),
+        # gated, flags already published (pure gating cost, all CUs computing)
+        "preset": lambda i: ops.ag_gemm(None, A_full, B, C, flags_pub, order_d, epoch=2 ** 30, num_producers=0),
+    }, steps, warmup)
+    ms, ms_dedicated, ms_ungated, ms_preset = r["gated"], r["dedicated"], r["ungated"], r["preset"]
     extra["ag_gemm"] = {
         "shape": [cfg.M, cfg.N, cfg.K], "producers": producers,
         "us_gated_producer": ms * 1e3, "us_ungated": ms_ungated * 1e3, "us_gated_flags_preset": ms_preset * 1e3,
+        "us_gated_32_dedicated_producers": ms_dedicated * 1e3,
         "tflops_gated_producer": flops / ms / 1e9, "tflops_ungated": flops / ms_ungated / 1e9,
         "gating_overhead_producer": ms / ms_ungated - 1.0, "gating_overhead_flag_check": ms_preset / ms_ungated - 1.0,
         "staging_bytes": 2 * A.numel() * 2,
@@ -103,12 +123,18 @@ def bench_rs(steps, warmup, producers, extra):
     out = torch.empty((rows, cfg.N), dtype=torch.bfloat16, device="cuda")
     recv = torch.empty_like(peers)
     flags = torch.zeros((cfg.world - 1) * rows // 128, dtype=torch.int32, device="cuda")
+    counters = torch.zeros_like(flags)
     order_d = torch.from_numpy(order).to("cuda")
     flops = 2.0 * cfg.M * cfg.N * cfg.K
-    t = Timer()
-    ms = t.run(lambda i: ops.gemm_rs(A, B, work, out, peers, recv, cfg.world, cfg.rank, flags, order_d, epoch=i + 1,
-                                     num_producers=producers), steps, warmup)
-    ms_plain = t.run(lambda i: ops.gemm(A, B, work), steps, warmup)
+    epoch = [0]
+
+    def rs(i):
+        epoch[0] += 1  # monotonic: flags and counters are never reset
+        ops.gemm_rs(A, B, work, out, peers, recv, cfg.world, cfg.rank, flags, order_d, epoch=epoch[0],
+                    num_producers=producers, stage_counters=counters)
+
+    r = interleaved({"rs": rs, "plain": lambda i: ops.gemm(A, B, work)}, steps, warmup)
+    ms, ms_plain = r["rs"], r["plain"]
     extra["gemm_rs"] = {"shape": [cfg.M, cfg.N, cfg.K], "producers": producers, "us": ms * 1e3,
                         "tflops": flops / ms / 1e9, "us_plain_gemm_same_shape": ms_plain * 1e3,
                         "epilogue_bytes_read": peers.numel() * 2}
@@ -134,16 +160,19 @@ def bench_moe(steps, warmup, extra):
 
     def dispatch_gemm(i):
         ops.moe_permute(tokens, d["pull_indices"], post)
-        ops.moe_grouped_gemm(post, w1, h, rb_expert=d["rb_expert"], mode=0)
+        ops.moe_grouped_gemm(post, w1, h, rb_expert=d["rb_expert"], mode=0, rb_rows=d["rb_rows"])
 
     ms4 = t.run(dispatch_gemm, steps, warmup)
     ms_perm = t.run(lambda i: ops.moe_permute(tokens, d["pull_indices"], post), steps, warmup)
-    ms_g1 = t.run(lambda i: ops.moe_grouped_gemm(post, w1, act, rb_expert=d["rb_expert"], mode=1), steps, warmup)
-    ms_g2 = t.run(lambda i: ops.moe_grouped_gemm(act, w2, ye, rb_expert=d["rb_expert"], mode=0), steps, warmup)
+    ms_g1 = t.run(lambda i: ops.moe_grouped_gemm(post, w1, act, rb_expert=d["rb_expert"], mode=1,
+                                                 rb_rows=d["rb_rows"]), steps, warmup)
+    ms_g2 = t.run(lambda i: ops.moe_grouped_gemm(act, w2, ye, rb_expert=d["rb_expert"], mode=0,
+                                                 rb_rows=d["rb_rows"]), steps, warmup)
     ms_comb = t.run(lambda i: ops.moe_combine(ye, d["row_weight"], d["owner_offset"], d["slot_to_row"], y),
                     steps, warmup)
     ms5 = t.run(lambda i: ops.moe_ffn_combine(tokens, d["pull_indices"], d["row_weight"], d["owner_offset"],
-                                              d["slot_to_row"], w1, w2, post, act, ye, y, rb_expert=d["rb_expert"]),
+                                              d["slot_to_row"], w1, w2, post, act, ye, y, rb_expert=d["rb_expert"],
+                                              rb_rows=d["rb_rows"]),
                 steps, warmup)
     used = idx["padded_tokens_per_expert"] > 0
     w_bytes1 = int(used.sum()) * cfg.H * 2 * cfg.I * 2
@@ -194,9 +223,10 @@ def load_traffic():
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--producers", type=int, default=32)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--producers", type=int, default=-1,
+                    help="-1: cooperative staging by every workgroup; >0: dedicated producer workgroups")
     ap.add_argument("--workload", default="all", choices=["all", "ag", "gemm", "rs", "moe", "calib"])
     ap.add_argument("--no-cpu", action="store_true")
     args = ap.parse_args()
@@ -220,7 +250,7 @@ def main():
             "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
             "dtype": "bf16", "data": "synthetic (seeded N(0,1)/sqrt(K) bf16; seeded random stage order)",
             "config": {"workload": "ag_gemm: one TP=8 rank's share, A_full 16384x8192 (8 staged shards), "
-                                   "B 8192x3584, C 16384x3584, 128-row flags, in-launch producer role",
+                                   "B 8192x3584, C 16384x3584, 128-row flags, staged in-launch (producer role)",
                        "M": 16384, "N": 3584, "K": 8192, "producers": args.producers, "parallelism": "tp8-rank-share"},
             "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                          "frac": round(tflops / PEAK_BF16_TFLOPS, 4), "traffic": load_traffic()},

@@ -64,7 +64,13 @@ int mk_gemm(const mk_gemm_args* args, void* stream);
  * wait of fused_comp_sm (src/ag_gemm.cu:374-377).
  *   gated == 0             : plain GEMM on A_full, no flags read (baseline)
  *   gated, producers == 0  : flags are published by someone else
- *   gated, producers  > 0  : producer role runs inside the same launch     */
+ *   gated, producers  > 0  : that many producer workgroups run inside the
+ *                            launch beside the compute workgroups
+ *   gated, producers == -1 : cooperative staging — every workgroup first
+ *                            copies its share of 128 KB pieces (in stage
+ *                            order), counting pieces per tile in
+ *                            stage_counters; the workgroup that completes a
+ *                            tile publishes its flag; then all compute    */
 typedef struct mk_ag_gemm_args {
   const void* A_shards;  /* bf16 [M, K]: shards stacked in rank order (source) */
   void* A_full;          /* bf16 [M, K]: gathered A (destination / GEMM input) */
@@ -79,6 +85,7 @@ typedef struct mk_ag_gemm_args {
   int32_t num_cus;              /* total workgroups (producers + compute); 0 = all CUs */
   uint32_t spin_limit;          /* polls before a wait gives up; 0 = unbounded */
   uint32_t* error_word;         /* optional device word, bit0 set on timeout */
+  uint32_t* stage_counters;     /* [M/128] piece counters for producers == -1; zero once, never reset */
 } mk_ag_gemm_args;
 int mk_ag_gemm(const mk_ag_gemm_args* args, void* stream);
 
@@ -106,10 +113,11 @@ typedef struct mk_gemm_rs_args {
   const int32_t* stage_order;   /* [(world-1) * (M/world)/128]; NULL = ascending */
   uint32_t epoch;
   int32_t gated;
-  int32_t num_producers;
+  int32_t num_producers;        /* as in mk_ag_gemm (-1 = cooperative staging) */
   int32_t num_cus;
   uint32_t spin_limit;
   uint32_t* error_word;
+  uint32_t* stage_counters;     /* [(world-1) * (M/world)/128] for producers == -1 */
 } mk_gemm_rs_args;
 int mk_gemm_rs(const mk_gemm_rs_args* args, void* stream);
 
@@ -133,6 +141,7 @@ typedef struct mk_moe_index {
   int32_t* pull_indices;             /* [R_pad, 3] (src_node, src_dev, src_token) */
   int32_t* row_expert;               /* [R_pad] local expert of each row */
   int32_t* rb_expert;                /* [R_pad / row_block] */
+  int32_t* rb_rows;                  /* [R_pad / row_block] real (non-padding) rows per row block */
   float* row_weight;                 /* [R_pad] gate of each row; 0 on padding */
   int32_t* owner_offset;             /* [num_tokens + 1] CSR over source tokens */
   int32_t* row_to_slot;              /* [R_pad] slot of each row; 0 on padding */
@@ -173,6 +182,8 @@ typedef struct mk_moe_grouped_gemm_args {
   void* out;                  /* bf16 [R_pad, N_out] */
   const int32_t* rb_expert;   /* [R_pad/128] device, or NULL */
   const int32_t* padded_tokens_per_expert; /* [E] device; used when rb_expert is NULL */
+  const int32_t* rb_rows;     /* [R_pad/128] real rows per row block, or NULL; lets the
+                                 kernel skip MFMAs of all-padding 32-row blocks */
   int64_t R_pad, K, Nw;       /* Nw = W's column count (2I in mode 1) */
   int32_t num_experts;
   int32_t mode;
@@ -203,6 +214,10 @@ int mk_moe_combine(const mk_moe_combine_args* args, void* stream);
 int mk_moe_invert_slots(const int32_t* row_to_slot, const int32_t* row_to_owner, int64_t R_pad,
                         int32_t* slot_to_row, void* stream);
 
+/* rb_rows[b] = number of rows r in [128b, 128b+128) with pull_indices[r][0] >= 0
+ * (device, from the reference's pull table). */
+int mk_moe_tile_rows(const int32_t* pull_indices, int64_t R_pad, int32_t* rb_rows, void* stream);
+
 /* The whole local MoE layer in one call: permute -> grouped GEMM1 + SwiGLU ->
  * grouped GEMM2 -> combine (four launches on `stream`).
  * Replaces moe_dispatch_gemm_glu_combine_fused
@@ -212,6 +227,7 @@ typedef struct mk_moe_ffn_args {
   const int32_t* pull_indices;  /* [R_pad, 3] */
   const int32_t* rb_expert;     /* [R_pad/128], or NULL */
   const int32_t* padded_tokens_per_expert; /* [E]; used when rb_expert is NULL */
+  const int32_t* rb_rows;       /* [R_pad/128] real rows per row block, or NULL */
   const float* row_weight;      /* [R_pad] */
   const int32_t* owner_offset;  /* [num_tokens + 1] */
   const int32_t* slot_to_row;   /* [R] */

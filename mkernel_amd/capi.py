@@ -24,6 +24,7 @@ EXPORTS = (
     "mk_moe_grouped_gemm",
     "mk_moe_combine",
     "mk_moe_invert_slots",
+    "mk_moe_tile_rows",
     "mk_moe_ffn_combine",
     "mk_query_workspace_bytes",
     "mk_device_cu_count",
@@ -55,19 +56,21 @@ class AgGemmArgs(C.Structure):
     _fields_ = [("A_shards", vp), ("A_full", vp), ("B", vp), ("C", vp),
                 ("M", i64), ("N", i64), ("K", i64),
                 ("flags", vp), ("stage_order", vp), ("epoch", u32), ("gated", i32),
-                ("num_producers", i32), ("num_cus", i32), ("spin_limit", u32), ("error_word", vp)]
+                ("num_producers", i32), ("num_cus", i32), ("spin_limit", u32), ("error_word", vp),
+                ("stage_counters", vp)]
 
 
 class GemmRsArgs(C.Structure):
     _fields_ = [("A", vp), ("B", vp), ("workspace", vp), ("output", vp), ("peer_src", vp),
                 ("peer_recv", vp), ("M", i64), ("N", i64), ("K", i64), ("world", i32), ("rank", i32),
                 ("flags", vp), ("stage_order", vp), ("epoch", u32), ("gated", i32),
-                ("num_producers", i32), ("num_cus", i32), ("spin_limit", u32), ("error_word", vp)]
+                ("num_producers", i32), ("num_cus", i32), ("spin_limit", u32), ("error_word", vp),
+                ("stage_counters", vp)]
 
 
 class MoeIndex(C.Structure):
     _fields_ = [("padded_tokens_per_expert", vp), ("local_rb_per_expert", vp), ("pull_indices", vp),
-                ("row_expert", vp), ("rb_expert", vp), ("row_weight", vp), ("owner_offset", vp),
+                ("row_expert", vp), ("rb_expert", vp), ("rb_rows", vp), ("row_weight", vp), ("owner_offset", vp),
                 ("row_to_slot", vp), ("row_to_owner", vp), ("slot_to_row", vp)]
 
 
@@ -78,7 +81,7 @@ class MoePermuteArgs(C.Structure):
 
 class MoeGroupedGemmArgs(C.Structure):
     _fields_ = [("A", vp), ("W", vp), ("out", vp), ("rb_expert", vp), ("padded_tokens_per_expert", vp),
-                ("R_pad", i64), ("K", i64),
+                ("rb_rows", vp), ("R_pad", i64), ("K", i64),
                 ("Nw", i64), ("num_experts", i32), ("mode", i32), ("num_cus", i32)]
 
 
@@ -89,7 +92,7 @@ class MoeCombineArgs(C.Structure):
 
 class MoeFfnArgs(C.Structure):
     _fields_ = [("tokens", vp), ("pull_indices", vp), ("rb_expert", vp), ("padded_tokens_per_expert", vp),
-                ("row_weight", vp),
+                ("rb_rows", vp), ("row_weight", vp),
                 ("owner_offset", vp), ("slot_to_row", vp), ("w1", vp), ("w2", vp), ("post_tokens", vp),
                 ("act", vp), ("y_expert", vp), ("y_out", vp), ("num_tokens", i64), ("n_src_rows", i64),
                 ("R_pad", i64), ("H", i64), ("I", i64), ("num_experts", i32), ("tokens_per_src", i32),
@@ -117,6 +120,8 @@ def lib() -> C.CDLL:
         L.mk_moe_build_indices.restype = C.c_int
         L.mk_moe_invert_slots.argtypes = [vp, vp, i64, vp, vp]
         L.mk_moe_invert_slots.restype = C.c_int
+        L.mk_moe_tile_rows.argtypes = [vp, i64, vp, vp]
+        L.mk_moe_tile_rows.restype = C.c_int
         L.mk_query_workspace_bytes.argtypes = [i32, i64, i64, i64]
         L.mk_query_workspace_bytes.restype = i64
         L.mk_device_cu_count.argtypes = []

@@ -152,11 +152,13 @@ int mk_ag_gemm(const mk_ag_gemm_args* a, void* stream) {
     if (nflags + a->M / bm > 8192)
       return fail(MK_ESHAPE, "mk_ag_gemm: too many flags for the schedule scratch");
   }
-  if (a->num_producers < 0) return fail(MK_EINVAL, "mk_ag_gemm: num_producers < 0");
-  if (a->gated && a->num_producers > 0 && !a->A_shards)
-    return fail(MK_EINVAL, "mk_ag_gemm: producers need A_shards");
+  if (a->num_producers < -1) return fail(MK_EINVAL, "mk_ag_gemm: num_producers must be >= -1");
+  if (a->gated && a->num_producers != 0 && !a->A_shards)
+    return fail(MK_EINVAL, "mk_ag_gemm: staging needs A_shards");
+  const bool coop = a->gated && a->num_producers == -1;
+  if (coop && !a->stage_counters) return fail(MK_EINVAL, "mk_ag_gemm: cooperative staging needs stage_counters");
   const int total = a->num_cus > 0 ? a->num_cus : d.cus;
-  const int n_prod = a->gated ? a->num_producers : 0;
+  const int n_prod = (a->gated && a->num_producers > 0) ? a->num_producers : 0;
   if (n_prod >= total) return fail(MK_EINVAL, "mk_ag_gemm: num_producers (%d) leaves no compute workgroups", n_prod);
   mk::GemmKParams p;
   fill_common(p);
@@ -175,13 +177,16 @@ int mk_ag_gemm(const mk_ag_gemm_args* a, void* stream) {
     p.a_flags = a->flags;
     p.a_stage_order = a->stage_order;
     p.perm_mode = a->stage_order ? mk::kPermArrival : mk::kPermNone;
-    if (n_prod > 0) {
+    if (n_prod > 0 || coop) {
       p.st_src = static_cast<const uint16_t*>(a->A_shards);
       p.st_dst = static_cast<uint16_t*>(a->A_full);
       p.st_cols = (int)a->K;
       p.st_nblocks = (int)nflags;
       p.st_order = a->stage_order;
       p.st_flags = a->flags;
+      p.st_counters = a->stage_counters;
+      p.st_coop = coop ? 1 : 0;
+      p.st_batch = 8;
     }
   }
   hipError_t e = mk::launch_gemm(p, bm, mk::kEpiStore, static_cast<hipStream_t>(stream));
@@ -202,13 +207,16 @@ int mk_gemm_rs(const mk_gemm_rs_args* a, void* stream) {
   if (npeers > 0 && !a->peer_recv) return fail(MK_EINVAL, "mk_gemm_rs: peer_recv is null");
   const int own_rows = (int)(a->M / a->world);
   const int total = a->num_cus > 0 ? a->num_cus : d.cus;
-  const int n_prod = (a->gated && npeers > 0) ? a->num_producers : 0;
+  if (a->num_producers < -1) return fail(MK_EINVAL, "mk_gemm_rs: num_producers must be >= -1");
+  const bool coop = a->gated && npeers > 0 && a->num_producers == -1;
+  const int n_prod = (a->gated && npeers > 0 && a->num_producers > 0) ? a->num_producers : 0;
   if (a->gated && npeers > 0) {
     if (!a->flags) return fail(MK_EINVAL, "mk_gemm_rs: gated launch needs flags");
     if (a->epoch == 0) return fail(MK_EINVAL, "mk_gemm_rs: epoch 0 is reserved");
-    if (n_prod > 0 && !a->peer_src) return fail(MK_EINVAL, "mk_gemm_rs: producers need peer_src");
+    if (a->num_producers != 0 && !a->peer_src) return fail(MK_EINVAL, "mk_gemm_rs: staging needs peer_src");
+    if (coop && !a->stage_counters) return fail(MK_EINVAL, "mk_gemm_rs: cooperative staging needs stage_counters");
   }
-  if (n_prod < 0 || n_prod >= total) return fail(MK_EINVAL, "mk_gemm_rs: bad num_producers");
+  if (n_prod >= total) return fail(MK_EINVAL, "mk_gemm_rs: bad num_producers");
   mk::GemmKParams p;
   fill_common(p);
   p.A = static_cast<const uint16_t*>(a->A);
@@ -230,13 +238,16 @@ int mk_gemm_rs(const mk_gemm_rs_args* a, void* stream) {
   p.err = a->error_word;
   if (a->gated && npeers > 0) {
     p.rs_flags = a->flags;
-    if (n_prod > 0) {
+    if (n_prod > 0 || coop) {
       p.st_src = static_cast<const uint16_t*>(a->peer_src);
       p.st_dst = static_cast<uint16_t*>(a->peer_recv);
       p.st_cols = (int)a->N;
       p.st_nblocks = npeers * (own_rows / 128);
       p.st_order = a->stage_order;
       p.st_flags = a->flags;
+      p.st_counters = a->stage_counters;
+      p.st_coop = coop ? 1 : 0;
+      p.st_batch = 8;
     }
   }
   hipError_t e = mk::launch_gemm(p, bm, mk::kEpiReduce, static_cast<hipStream_t>(stream));
@@ -297,6 +308,10 @@ int mk_moe_build_indices(const int32_t* topk_ids, const float* gates, int32_t T,
       }
       if (o->row_expert) o->row_expert[r] = e;
       if (o->rb_expert && (r % row_block) == 0) o->rb_expert[r / row_block] = e;
+      if (o->rb_rows) {
+        if ((r % row_block) == 0) o->rb_rows[r / row_block] = 0;
+        if (real) ++o->rb_rows[r / row_block];
+      }
       if (o->row_weight) o->row_weight[r] = real ? gates[(int64_t)t * topk + e2t[e][i].second] : 0.f;
       if (real) ++owner_count[t];
     }
@@ -342,8 +357,8 @@ int mk_moe_permute(const mk_moe_permute_args* a, void* stream) {
 }
 
 static int grouped_gemm_impl(const void* A, const void* W, void* out, const int32_t* rb_expert,
-                             const int32_t* expert_rows, int64_t R_pad, int64_t K, int64_t Nw, int32_t E,
-                             int32_t mode, int32_t num_cus, hipStream_t stream) {
+                             const int32_t* expert_rows, const int32_t* rb_rows, int64_t R_pad, int64_t K,
+                             int64_t Nw, int32_t E, int32_t mode, int32_t num_cus, hipStream_t stream) {
   if (!A || !W || !out || (!rb_expert && !expert_rows)) return fail(MK_EINVAL, "mk_moe_grouped_gemm: null argument");
   if (mode != 0 && mode != 1) return fail(MK_EINVAL, "mk_moe_grouped_gemm: mode must be 0 or 1");
   if (E <= 0) return fail(MK_EINVAL, "mk_moe_grouped_gemm: num_experts must be positive");
@@ -363,6 +378,7 @@ static int grouped_gemm_impl(const void* A, const void* W, void* out, const int3
   p.tiles_n = (int)(Nw / 256);
   p.rb_expert = rb_expert;
   p.expert_rows = expert_rows;
+  p.rb_rows = rb_rows;
   p.n_experts = E;
   p.swiglu_I = (int)(Nw / 2);
   const int total = num_cus > 0 ? num_cus : d.cus;
@@ -373,7 +389,7 @@ static int grouped_gemm_impl(const void* A, const void* W, void* out, const int3
 
 int mk_moe_grouped_gemm(const mk_moe_grouped_gemm_args* a, void* stream) {
   if (!a) return fail(MK_EINVAL, "mk_moe_grouped_gemm: null argument");
-  return grouped_gemm_impl(a->A, a->W, a->out, a->rb_expert, a->padded_tokens_per_expert, a->R_pad, a->K, a->Nw, a->num_experts, a->mode,
+  return grouped_gemm_impl(a->A, a->W, a->out, a->rb_expert, a->padded_tokens_per_expert, a->rb_rows, a->R_pad, a->K, a->Nw, a->num_experts, a->mode,
                            a->num_cus, static_cast<hipStream_t>(stream));
 }
 
@@ -401,6 +417,15 @@ int mk_moe_invert_slots(const int32_t* row_to_slot, const int32_t* row_to_owner,
   return e == hipSuccess ? MK_OK : hip_fail(e, "mk_moe_invert_slots launch");
 }
 
+int mk_moe_tile_rows(const int32_t* pull_indices, int64_t R_pad, int32_t* rb_rows, void* stream) {
+  if (!pull_indices || (!rb_rows && R_pad > 0)) return fail(MK_EINVAL, "mk_moe_tile_rows: null argument");
+  if (R_pad < 0 || R_pad % 128) return fail(MK_ESHAPE, "mk_moe_tile_rows: R_pad must be a multiple of 128");
+  DevInfo d;
+  if (int rc = device_info(&d)) return rc;
+  hipError_t e = mk::launch_tile_rows(pull_indices, R_pad, rb_rows, static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? MK_OK : hip_fail(e, "mk_moe_tile_rows launch");
+}
+
 int mk_moe_ffn_combine(const mk_moe_ffn_args* a, void* stream) {
   if (!a) return fail(MK_EINVAL, "mk_moe_ffn_combine: null argument");
   if (a->I % 128) return fail(MK_ESHAPE, "mk_moe_ffn_combine: I must be a multiple of 128");
@@ -408,10 +433,12 @@ int mk_moe_ffn_combine(const mk_moe_ffn_args* a, void* stream) {
   mk_moe_permute_args pa{a->tokens, a->pull_indices, a->post_tokens, a->R_pad, a->H,
                          a->n_src_rows, a->tokens_per_src, a->devs_per_node};
   if (int rc = mk_moe_permute(&pa, stream)) return rc;
-  if (int rc = grouped_gemm_impl(a->post_tokens, a->w1, a->act, a->rb_expert, a->padded_tokens_per_expert, a->R_pad,
+  if (int rc = grouped_gemm_impl(a->post_tokens, a->w1, a->act, a->rb_expert, a->padded_tokens_per_expert,
+                                 a->rb_rows, a->R_pad,
                                  a->H, 2 * a->I, a->num_experts, 1, a->num_cus, s))
     return rc;
-  if (int rc = grouped_gemm_impl(a->act, a->w2, a->y_expert, a->rb_expert, a->padded_tokens_per_expert, a->R_pad,
+  if (int rc = grouped_gemm_impl(a->act, a->w2, a->y_expert, a->rb_expert, a->padded_tokens_per_expert,
+                                 a->rb_rows, a->R_pad,
                                  a->I, a->H, a->num_experts, 0, a->num_cus, s))
     return rc;
   mk_moe_combine_args ca{a->y_expert, a->row_weight, a->owner_offset, a->slot_to_row, a->y_out,

@@ -115,9 +115,64 @@ __device__ void producer_role(const GemmKParams& p, int pid) {
       for (int u = 0; u < U; ++u) __builtin_nontemporal_store(v[u], dst + base + u * NT);
     }
     for (; base < block_vec; base += NT) __builtin_nontemporal_store(__builtin_nontemporal_load(src + base), dst + base);
-    __threadfence();
+    // The barrier waits for every wave's stores; thread 0's agent-scope
+    // release then makes the whole block visible (one L2 write-back per
+    // block, not one per wave).
     __syncthreads();
     if (threadIdx.x == 0) publish_flag(p.st_flags + b, p.epoch);
+  }
+}
+
+// Cooperative staging: every compute workgroup copies its share of the
+// staging pieces (kPieces per 128-row block, taken in stage order so the
+// earliest-needed blocks complete first) before it starts computing.  Each
+// finished piece bumps its block's counter; the workgroup whose increment
+// completes the block publishes the block's flag.  Counters are never reset:
+// completion is detected modulo kPieces.
+template <int NT>
+__device__ void coop_stage(const GemmKParams& p, int cid) {
+  const int64_t block_elems = (int64_t)kFlagRows * p.st_cols;
+  const int64_t piece_vec = block_elems / 8 / kPieces;  // 16-byte units per piece
+  const int total = p.st_nblocks * kPieces;
+  constexpr int U = 16;
+  auto copy_piece = [&](int q) {
+    const int pos = q / kPieces, piece = q % kPieces;
+    const int b = p.st_order ? p.st_order[pos] : pos;
+    const u32x4_t* src = reinterpret_cast<const u32x4_t*>(p.st_src + (int64_t)b * block_elems) + piece * piece_vec;
+    u32x4_t* dst = reinterpret_cast<u32x4_t*>(p.st_dst + (int64_t)b * block_elems) + piece * piece_vec;
+    int64_t base = threadIdx.x;
+    for (; base + (int64_t)(U - 1) * NT < piece_vec; base += (int64_t)U * NT) {
+      u32x4_t v[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) v[u] = __builtin_nontemporal_load(src + base + u * NT);
+#pragma unroll
+      for (int u = 0; u < U; ++u) __builtin_nontemporal_store(v[u], dst + base + u * NT);
+    }
+    for (; base < piece_vec; base += NT) __builtin_nontemporal_store(__builtin_nontemporal_load(src + base), dst + base);
+    return b;
+  };
+  auto count_piece = [&](int b) {
+    const uint32_t old = __hip_atomic_fetch_add(p.st_counters + b, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (old % kPieces == kPieces - 1) {
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+      publish_flag(p.st_flags + b, p.epoch);
+    }
+  };
+  // Pieces are released in batches of p.st_batch: copy the batch, one
+  // barrier, one agent-scope release (an L2 write-back), then count the
+  // batch's pieces.  Fewer releases cost fewer serialised write-backs; the
+  // first batch is a single piece so the earliest blocks complete early.
+  int q = cid, batch = 1;
+  while (q < total) {
+    int bs[8];
+    int n = 0;
+    for (; n < batch && q < total; ++n, q += p.n_cons) bs[n] = copy_piece(q);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+      for (int i = 0; i < n; ++i) count_piece(bs[i]);
+    }
+    batch = p.st_batch;
   }
 }
 
@@ -337,6 +392,15 @@ __device__ void compute_role(const GemmKParams& p, int cons_id, char* smem, cons
       Bp += (int64_t)e * p.b_expert_stride;
     }
 
+    // Row tiles padded past their expert's real rows: each wave skips the
+    // MFMAs of its 32-row blocks that hold padding only (their outputs stay
+    // zero, as they would be from the zero-filled padding rows).
+    int fm_active = C::FM;
+    if (p.rb_rows) {
+      const int real = __builtin_amdgcn_readfirstlane(p.rb_rows[tm]) - wm * C::WTM;
+      fm_active = __builtin_amdgcn_readfirstlane(min(max((real + 31) / 32, 0), C::FM));
+    }
+
     // Flag gate on the A rows of this tile (AllGather consumer side).
     if (p.a_flags) {
       if (tid == 0)
@@ -399,9 +463,11 @@ __device__ void compute_role(const GemmKParams& p, int cons_id, char* smem, cons
     auto mfma = [&](int kk) {
 #pragma unroll
       for (int i = 0; i < C::FM; ++i)
+        if (i < fm_active) {
 #pragma unroll
-        for (int j = 0; j < C::FN; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[kk][j], af[kk][i], acc[i][j], 0, 0, 0);
+          for (int j = 0; j < C::FN; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[kk][j], af[kk][i], acc[i][j], 0, 0, 0);
+        }
     };
 
     // Prologue: fill the whole ring, wait for stage 0, read its kk = 0.
@@ -415,18 +481,22 @@ __device__ void compute_role(const GemmKParams& p, int cons_id, char* smem, cons
     // Steady state for stage kt (ring slot kt % S):
     //   read kk=1 operands | MFMA kk=0 | wait stage kt+1 + barrier |
     //   refill the slot with stage kt+S | read stage kt+1 kk=0 | MFMA kk=1
-    // so the barrier and the LDS reads overlap MFMAs already issued.
-    for (int kt = 0; kt < nk; ++kt) {
+    // so the barrier and the LDS reads overlap MFMAs already issued.  The
+    // last stage is peeled off: with no branch around the barrier block the
+    // compiler's LDS wait counts stay exact, and the kk=1 MFMAs do not wait
+    // for the next stage's reads.
+    for (int kt = 0; kt < nk - 1; ++kt) {
       read_frags(kt % C::S, 1);
       mfma(0);
-      if (kt + 1 < nk) {
-        wait_stage<C::S + 1, C::LOADS>(min(C::S - 1, nk - 1 - kt) - 1);
-        __syncthreads();
-        if (kt + C::S < nk) issue(kt + C::S);
-        read_frags((kt + 1) % C::S, 0);
-      }
+      wait_stage<C::S + 1, C::LOADS>(min(C::S - 1, nk - 1 - kt) - 1);
+      __syncthreads();
+      if (kt + C::S < nk) issue(kt + C::S);
+      read_frags((kt + 1) % C::S, 0);
       mfma(1);
     }
+    read_frags((nk - 1) % C::S, 1);
+    mfma(0);
+    mfma(1);
     // Every wave must be done with the ring before the next tile's DMA.
     __syncthreads();
     store_tile<C, EPI>(p, acc, m0, tn, tid);
@@ -485,6 +555,7 @@ __global__ __launch_bounds__(64 * WAVES, 1) void gemm_kernel(GemmKParams p) {
     return;
   }
   int cons = blockIdx.x - p.n_prod;
+  if (p.st_coop) coop_stage<C::NT>(p, cons);
   // XCD-aware renumbering: workgroups are dealt round-robin to the 8 XCDs,
   // so give each XCD a contiguous run of consumer ids (hence of tiles, which
   // the grouped order keeps close in A rows / B columns) for L2 reuse.

@@ -9,6 +9,7 @@ namespace mk {
 enum Epilogue : int { kEpiStore = 0, kEpiSwiGLU = 1, kEpiReduce = 2 };
 enum PermMode : int { kPermNone = 0, kPermArrival = 1, kPermOwnedLast = 2 };
 constexpr int kMaxTilesM = 512;
+constexpr int kPieces = 16;  // cooperative staging: pieces per 128-row block
 
 struct GemmKParams {
   // operands
@@ -27,6 +28,7 @@ struct GemmKParams {
   // grouped GEMM: expert of each BM row tile (nullptr = dense)
   const int* rb_expert;
   const int* expert_rows;   // padded rows per expert (used when rb_expert is null)
+  const int* rb_rows;       // real rows per 128-row tile (null: every row is real)
   int n_experts;
   // SwiGLU: width I of the gate half of B's columns
   int swiglu_I;
@@ -45,6 +47,9 @@ struct GemmKParams {
   int st_cols, st_nblocks;
   const int* st_order;
   uint32_t* st_flags;
+  uint32_t* st_counters;    // cooperative staging: pieces completed per block (mod kPieces)
+  int st_coop;              // 1: every workgroup stages its pieces before computing
+  int st_batch;             // pieces per release after the first (1..8)
   // flag protocol
   uint32_t epoch;
   uint32_t spin_limit;
@@ -72,6 +77,7 @@ struct CombineKParams {
   int out_dtype;
 };
 hipError_t launch_combine(const CombineKParams& p, hipStream_t stream);
+hipError_t launch_tile_rows(const int* pull, int64_t R_pad, int* rb_rows, hipStream_t stream);
 hipError_t launch_invert_slots(const int* row_to_slot, const int* row_to_owner, int64_t R_pad, int* slot_to_row,
                                hipStream_t stream);
 

@@ -75,6 +75,20 @@ hipError_t launch_combine(const CombineKParams& p, hipStream_t stream) {
   return hipGetLastError();
 }
 
+// One workgroup per 128-row block: count rows with a real source token.
+__global__ __launch_bounds__(128) void tile_rows_kernel(const int* pull, int64_t R_pad, int* rb_rows) {
+  const int64_t r = (int64_t)blockIdx.x * 128 + threadIdx.x;
+  const int real = (r < R_pad && pull[3 * r] >= 0) ? 1 : 0;
+  const int n = __syncthreads_count(real);
+  if (threadIdx.x == 0) rb_rows[blockIdx.x] = n;
+}
+
+hipError_t launch_tile_rows(const int* pull, int64_t R_pad, int* rb_rows, hipStream_t stream) {
+  if (R_pad == 0) return hipSuccess;
+  hipLaunchKernelGGL(tile_rows_kernel, dim3((unsigned)((R_pad + 127) / 128)), dim3(128), 0, stream, pull, R_pad, rb_rows);
+  return hipGetLastError();
+}
+
 __global__ void invert_slots_kernel(const int* row_to_slot, const int* row_to_owner, int64_t R_pad,
                                     int* slot_to_row) {
   const int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;

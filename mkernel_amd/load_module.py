@@ -30,7 +30,19 @@ import torch
 
 from . import ops
 
-_DEFAULT_PRODUCERS = 32
+_DEFAULT_PRODUCERS = -1  # cooperative staging by every workgroup
+_COUNTERS: dict = {}
+
+
+def _counters(flags: torch.Tensor) -> torch.Tensor:
+    """Piece counters for cooperative staging, one per flag word; zeroed once
+    per flag buffer and kept for the life of the process."""
+    key = (flags.data_ptr(), flags.numel())
+    c = _COUNTERS.get(key)
+    if c is None:
+        c = torch.zeros(flags.numel(), dtype=torch.int32, device=flags.device)
+        _COUNTERS[key] = c
+    return c
 
 
 class DistBuffer:
@@ -135,7 +147,8 @@ def _ag_module():
         ``barrier`` word tile = epoch).  Pass ``A_recv=None`` when ``A.data_``
         is filled by someone else who also publishes the flags.  Producers:
         ``num_intra_comm_override`` if > 0, else 32.  ``active_sms`` caps the
-        grid (0 or >= CU count: every CU).  ``stage_order`` (int32 device
+        grid (0 or >= CU count: every CU).  The default (-1) stages
+        cooperatively: every workgroup copies its share first.  ``stage_order`` (int32 device
         tensor, optional) is the tile publication order the compute role
         follows."""
         Af = _data(A)
@@ -144,8 +157,9 @@ def _ag_module():
         producers = (num_intra_comm_override if num_intra_comm_override > 0 else _DEFAULT_PRODUCERS) if src is not None else 0
         cus = ops.cu_count()
         grid = active_sms if 0 < active_sms < cus else 0
-        ops.ag_gemm(src, Af, B, C, _flags(barrier, M // 128), stage_order, epoch=int(epoch), gated=True,
-                    num_producers=producers, num_cus=grid)
+        fl = _flags(barrier, M // 128)
+        ops.ag_gemm(src, Af, B, C, fl, stage_order, epoch=int(epoch), gated=True,
+                    num_producers=producers, num_cus=grid, stage_counters=_counters(fl))
         return C
 
     return _module("ag_gemm", s, ag_gemm_multinode=ag_gemm_multinode,
@@ -188,8 +202,9 @@ def _rs_module():
             recv = _DevicePtr(int(recv_buf_ptr))
         src = _data(staging) if staging is not None else None
         producers = (num_intra_comm if num_intra_comm > 0 else _DEFAULT_PRODUCERS) if src is not None else 0
-        ops.gemm_rs(A, B, _data(workspace), out, src, recv, world, rank, _flags(barrier, max(nflags, 1)),
-                    stage_order, epoch=int(epoch), gated=True, num_producers=producers)
+        fl = _flags(barrier, max(nflags, 1))
+        ops.gemm_rs(A, B, _data(workspace), out, src, recv, world, rank, fl, stage_order, epoch=int(epoch),
+                    gated=True, num_producers=producers, stage_counters=_counters(fl))
         return out
 
     return _module("gemm_rs", s, gemm_rs_fused=gemm_rs_fused, prepare_epoch=s.prepare_epoch,
@@ -225,9 +240,11 @@ def _dispatch_module():
         ``padded_tokens_per_expert``."""
         tok = _data(pre_tokens)[:num_local_tokens]
         post = post_tokens[:num_padded_local_tokens]
+        rb_rows = torch.empty(max(num_padded_local_tokens // 128, 1), dtype=torch.int32, device=post.device)
+        ops.moe_tile_rows(pull_dispatch_indices[:num_padded_local_tokens], rb_rows)
         ops.moe_permute(tok, pull_dispatch_indices, post, tokens_per_src=num_local_tokens)
         ops.moe_grouped_gemm(post, weights, outputs[:num_padded_local_tokens],
-                             padded_tokens_per_expert=padded_tokens_per_expert, mode=0)
+                             padded_tokens_per_expert=padded_tokens_per_expert, mode=0, rb_rows=rb_rows)
         return outputs
 
     return _module("dispatch_gemm", s, moe_dispatch_gemm_fused=moe_dispatch_gemm_fused)
@@ -260,9 +277,12 @@ def _glu_module():
         # every slot index is < R <= R_pad, so R_pad entries always suffice
         slot_to_row = torch.empty(max(R_pad, 1), dtype=torch.int32, device=row_to_slot.device)
         ops.moe_invert_slots(row_to_slot[:R_pad], row_to_owner[:R_pad], slot_to_row)
+        rb_rows = torch.empty(max(R_pad // 128, 1), dtype=torch.int32, device=row_to_slot.device)
+        ops.moe_tile_rows(pull_dispatch_indices[:R_pad], rb_rows)
         ops.moe_ffn_combine(tok, pull_dispatch_indices, topk_weights, owner_offset, slot_to_row, w1, w2,
                             post_tokens[:R_pad], act[:R_pad], y_expert[:R_pad], yo[:num_local_tokens],
-                            padded_tokens_per_expert=padded_tokens_per_expert, tokens_per_src=num_local_tokens)
+                            padded_tokens_per_expert=padded_tokens_per_expert, tokens_per_src=num_local_tokens,
+                            rb_rows=rb_rows)
         return yo
 
     return _module("dispatch_gemm_glu_combine", s, moe_dispatch_gemm_glu_combine_fused=moe_dispatch_gemm_glu_combine_fused,

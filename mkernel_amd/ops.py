@@ -47,27 +47,30 @@ def gemm(A: torch.Tensor, B: torch.Tensor, out: torch.Tensor | None = None, num_
 
 
 def ag_gemm(A_shards, A_full, B, C_out, flags, stage_order, epoch: int, gated: bool = True,
-            num_producers: int = 32, num_cus: int = 0, spin_limit: int = 0, error_word=None) -> torch.Tensor:
-    """Flag-gated AllGather+GEMM; see include/mk.h mk_ag_gemm."""
+            num_producers: int = -1, num_cus: int = 0, spin_limit: int = 0, error_word=None,
+            stage_counters=None) -> torch.Tensor:
+    """Flag-gated AllGather+GEMM; see include/mk.h mk_ag_gemm.  num_producers
+    -1 (default) stages cooperatively and needs stage_counters (int32
+    [M/128], zeroed once)."""
     _bf16(A_full, "A_full"); _bf16(B, "B"); _bf16(C_out, "C")
     M, K = A_full.shape
     N = B.shape[1]
     args = AgGemmArgs(_ptr(A_shards), _ptr(A_full), _ptr(B), _ptr(C_out), M, N, K, _ptr(flags), _ptr(stage_order),
-                      epoch, int(gated), num_producers, num_cus, spin_limit, _ptr(error_word))
+                      epoch, int(gated), num_producers, num_cus, spin_limit, _ptr(error_word), _ptr(stage_counters))
     capi.call("mk_ag_gemm", args, _stream())
     return C_out
 
 
 def gemm_rs(A, B, workspace, output, peer_src, peer_recv, world: int, rank: int, flags, stage_order, epoch: int,
-            gated: bool = True, num_producers: int = 16, num_cus: int = 0, spin_limit: int = 0,
-            error_word=None) -> torch.Tensor:
+            gated: bool = True, num_producers: int = -1, num_cus: int = 0, spin_limit: int = 0,
+            error_word=None, stage_counters=None) -> torch.Tensor:
     """GEMM with the reduce-scatter fold in the epilogue; see mk_gemm_rs."""
     _bf16(A, "A"); _bf16(B, "B")
     M, K = A.shape
     N = B.shape[1]
     args = GemmRsArgs(_ptr(A), _ptr(B), _ptr(workspace), _ptr(output), _ptr(peer_src), _ptr(peer_recv), M, N, K,
                       world, rank, _ptr(flags), _ptr(stage_order), epoch, int(gated), num_producers, num_cus,
-                      spin_limit, _ptr(error_word))
+                      spin_limit, _ptr(error_word), _ptr(stage_counters))
     capi.call("mk_gemm_rs", args, _stream())
     return output
 
@@ -89,6 +92,7 @@ def moe_build_indices(topk_ids: np.ndarray, gates: np.ndarray, e0: int, n_local:
         "pull_indices": np.zeros((Rp, 3), np.int32),
         "row_expert": np.zeros(Rp, np.int32),
         "rb_expert": np.zeros(Rp // row_block, np.int32),
+        "rb_rows": np.zeros(Rp // row_block, np.int32),
         "row_weight": np.zeros(Rp, np.float32),
         "owner_offset": np.zeros(T + 1, np.int32),
         "row_to_slot": np.zeros(Rp, np.int32),
@@ -111,15 +115,23 @@ def moe_permute(tokens, pull, post, tokens_per_src: int | None = None, devs_per_
     return post
 
 
-def moe_grouped_gemm(A, W, out, rb_expert=None, padded_tokens_per_expert=None, mode: int = 0, num_cus: int = 0):
+def moe_grouped_gemm(A, W, out, rb_expert=None, padded_tokens_per_expert=None, mode: int = 0, num_cus: int = 0,
+                     rb_rows=None):
     """mode 0: out = A @ W[e]; mode 1: out = silu(h[:, :I]) * h[:, I:], h = A @ W[e]."""
     _bf16(A, "A"); _bf16(W, "W"); _bf16(out, "out")
     R_pad, K = A.shape
     E, _, Nw = W.shape
-    args = MoeGroupedGemmArgs(_ptr(A), _ptr(W), _ptr(out), _ptr(rb_expert), _ptr(padded_tokens_per_expert), R_pad, K,
-                              Nw, E, mode, num_cus)
+    args = MoeGroupedGemmArgs(_ptr(A), _ptr(W), _ptr(out), _ptr(rb_expert), _ptr(padded_tokens_per_expert),
+                              _ptr(rb_rows), R_pad, K, Nw, E, mode, num_cus)
     capi.call("mk_moe_grouped_gemm", args, _stream())
     return out
+
+
+def moe_tile_rows(pull, rb_rows):
+    """rb_rows[b] = real rows in row block b (from the pull table)."""
+    capi.check("mk_moe_tile_rows", capi.lib().mk_moe_tile_rows(_ptr(pull), pull.shape[0], _ptr(rb_rows),
+                                                               C.c_void_p(_stream() or None)))
+    return rb_rows
 
 
 def moe_invert_slots(row_to_slot, row_to_owner, slot_to_row):
@@ -141,14 +153,15 @@ def moe_combine(y_expert, row_weight, owner_offset, slot_to_row, y_out):
 
 def moe_ffn_combine(tokens, pull, row_weight, owner_offset, slot_to_row, w1, w2, post, act, y_expert, y_out,
                     rb_expert=None, padded_tokens_per_expert=None, tokens_per_src: int | None = None,
-                    devs_per_node: int = 1, num_cus: int = 0):
+                    devs_per_node: int = 1, num_cus: int = 0, rb_rows=None):
     """permute -> grouped GEMM1 + SwiGLU -> grouped GEMM2 -> combine."""
     T, H = y_out.shape
     E, _, I2 = w1.shape
     R_pad = post.shape[0]
     od = 0 if y_out.dtype == torch.float32 else 1
     tps = tokens.shape[0] if tokens_per_src is None else tokens_per_src
-    args = MoeFfnArgs(_ptr(tokens), _ptr(pull), _ptr(rb_expert), _ptr(padded_tokens_per_expert), _ptr(row_weight),
+    args = MoeFfnArgs(_ptr(tokens), _ptr(pull), _ptr(rb_expert), _ptr(padded_tokens_per_expert), _ptr(rb_rows),
+                      _ptr(row_weight),
                       _ptr(owner_offset), _ptr(slot_to_row), _ptr(w1), _ptr(w2), _ptr(post), _ptr(act), _ptr(y_expert),
                       _ptr(y_out), T, tokens.shape[0], R_pad, H, I2 // 2, E, tps, devs_per_node, od, num_cus)
     capi.call("mk_moe_ffn_combine", args, _stream())

@@ -68,8 +68,10 @@ def build_indices_py(topk_ids, gates, e0: int, n_local: int, row_block: int = RO
     for r, (s, o) in enumerate(zip(row_to_slot, row_to_owner)):
         if o >= 0:
             slot_to_row[s] = r
+    rb_rows = [sum(1 for (sn, _, _) in pull[b:b + row_block] if sn >= 0) for b in range(0, len(pull), row_block)]
     return {
         "padded_tokens_per_expert": padded,
+        "rb_rows": rb_rows,
         "local_rb_per_expert": [len(l) // row_block for l in e2t],
         "pull_indices": pull,
         "row_expert": row_expert,
@@ -124,8 +126,10 @@ def build_indices_np(topk_ids: np.ndarray, gates: np.ndarray, e0: int, n_local: 
     row_to_owner[rows] = 0
     slot_to_row = np.zeros(R, dtype=np.int32)
     slot_to_row[row_to_slot[rows]] = rows
+    rb_rows = (pull[:, 0] >= 0).reshape(-1, row_block).sum(1).astype(np.int32) if R_pad else np.zeros(0, np.int32)
     return {
         "padded_tokens_per_expert": padded.astype(np.int32),
+        "rb_rows": rb_rows,
         "local_rb_per_expert": (cnt // row_block).astype(np.int32),
         "pull_indices": pull,
         "row_expert": row_expert,

@@ -30,8 +30,8 @@ def test_library_exports_every_declared_symbol():
     assert L.mk_abi_version() == 1
 
 
-@pytest.mark.parametrize("cls,nfields", [(capi.GemmArgs, 12), (capi.AgGemmArgs, 15), (capi.GemmRsArgs, 19),
-                                         (capi.MoeIndex, 10), (capi.MoeGroupedGemmArgs, 11)])
+@pytest.mark.parametrize("cls,nfields", [(capi.GemmArgs, 12), (capi.AgGemmArgs, 16), (capi.GemmRsArgs, 20),
+                                         (capi.MoeIndex, 11), (capi.MoeGroupedGemmArgs, 12)])
 def test_struct_layouts(cls, nfields):
     assert len(cls._fields_) == nfields
 
@@ -56,7 +56,7 @@ def test_index_builder_matches_oracle(T, rank):
     lib_o = ops.moe_build_indices(ids, gates, cfg.e0, cfg.n_local)
     ref = om.build_indices_np(ids, gates, cfg.e0, cfg.n_local)
     cref = build_indices_c(ids, gates, cfg.e0, cfg.n_local)
-    for key in ("padded_tokens_per_expert", "local_rb_per_expert", "pull_indices", "row_expert", "rb_expert",
+    for key in ("padded_tokens_per_expert", "local_rb_per_expert", "pull_indices", "row_expert", "rb_expert", "rb_rows",
                 "row_weight", "owner_offset", "row_to_slot", "row_to_owner", "slot_to_row"):
         assert np.array_equal(lib_o[key], ref[key]), key
         if key in cref:

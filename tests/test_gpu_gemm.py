@@ -78,15 +78,16 @@ def _ag_case(dev, world=8, shard=256, K=512, N=512, seed=0):
     return cfg, A, B, torch.from_numpy(order)
 
 
-@pytest.mark.parametrize("producers", [1, 4, 16])
+@pytest.mark.parametrize("producers", [-1, 1, 4, 16])
 def test_ag_gemm_producer_gated(dev, producers):
     _say(f"ag_gemm producers={producers}")
     cfg, A, B, order = _ag_case(dev)
     Ad, Bd = A.to(dev), B.to(dev)
     A_full = torch.zeros_like(Ad)
     flags = torch.zeros(cfg.M // 128, dtype=torch.int32, device=dev)
+    counters = torch.zeros(cfg.M // 128, dtype=torch.int32, device=dev)
     C = torch.empty((cfg.M, cfg.N), dtype=torch.bfloat16, device=dev)
-    ops.ag_gemm(Ad, A_full, Bd, C, flags, order.to(dev), epoch=1, num_producers=producers)
+    ops.ag_gemm(Ad, A_full, Bd, C, flags, order.to(dev), epoch=1, num_producers=producers, stage_counters=counters)
     torch.cuda.synchronize()
     assert torch.equal(A_full.cpu(), A)  # staging is a bit-exact copy
     assert (flags.cpu() == 1).all()
@@ -94,25 +95,29 @@ def test_ag_gemm_producer_gated(dev, producers):
     assert rel_fro(C.float(), ref) < TOL
     # flag order must not change the result (bit-equal to the ungated GEMM)
     C2 = torch.empty_like(C)
-    ops.ag_gemm(None, A_full, Bd, C2, None, None, epoch=1, gated=False)
+    ops.ag_gemm(None, A_full, Bd, C2, None, None, epoch=1, gated=False, num_producers=0)
     torch.cuda.synchronize()
     assert torch.equal(C.cpu(), C2.cpu())
 
 
 def test_ag_gemm_epochs_and_orders(dev):
-    """Several calls with increasing epochs and different stage orders, no
-    flag reset in between: every result is bit-identical."""
+    """Several calls with increasing (and skipped) epochs, different stage
+    orders and both staging modes, no flag or counter reset in between:
+    every result is bit-identical."""
     cfg, A, B, _ = _ag_case(dev)
     Ad, Bd = A.to(dev), B.to(dev)
     flags = torch.zeros(cfg.M // 128, dtype=torch.int32, device=dev)
+    counters = torch.zeros(cfg.M // 128, dtype=torch.int32, device=dev)
     outs = []
-    for epoch, seed in [(1, 5), (2, 6), (3, 7)]:
-        _say(f"ag_gemm epoch={epoch}")
+    for epoch, seed, prod in [(1, 5, -1), (2, 6, 8), (5, 7, -1), (6, 8, -1)]:
+        _say(f"ag_gemm epoch={epoch} producers={prod}")
         A_full = torch.zeros_like(Ad)
         order = torch.from_numpy(wl.stage_order(cfg.M // 128, seed)).to(dev)
         C = torch.empty((cfg.M, cfg.N), dtype=torch.bfloat16, device=dev)
-        ops.ag_gemm(Ad, A_full, Bd, C, flags, order, epoch=epoch, num_producers=8)
+        ops.ag_gemm(Ad, A_full, Bd, C, flags, order, epoch=epoch, num_producers=prod, stage_counters=counters)
         torch.cuda.synchronize()
+        assert torch.equal(A_full.cpu(), A)
+        assert (flags.cpu() == epoch).all()
         outs.append(C.cpu())
     assert all(torch.equal(outs[0], o) for o in outs[1:])
 
@@ -144,7 +149,7 @@ def test_ag_gemm_bounded_wait_reports_timeout(dev):
     assert rel_fro(C[:half].float(), gemm_ref(A[:half], B)) < TOL
 
 
-@pytest.mark.parametrize("rank,producers", [(0, 4), (3, 8), (7, 0)])
+@pytest.mark.parametrize("rank,producers", [(0, 4), (3, 8), (7, 0), (5, -1)])
 def test_gemm_rs_vs_oracle(dev, rank, producers):
     _say(f"gemm_rs rank={rank} producers={producers}")
     cfg = wl.RsCfg(world=8, rank=rank, M=2048, K=256, N=512)
@@ -160,8 +165,9 @@ def test_gemm_rs_vs_oracle(dev, rank, producers):
     else:
         recv = peers.to(dev)
         flags = torch.full((nfl,), 9, dtype=torch.int32, device=dev)
+    counters = torch.zeros(nfl, dtype=torch.int32, device=dev)
     ops.gemm_rs(Ad, Bd, work, out, peers.to(dev), recv, cfg.world, rank, flags, torch.from_numpy(order).to(dev),
-                epoch=9, num_producers=producers)
+                epoch=9, num_producers=producers, stage_counters=counters)
     torch.cuda.synchronize()
     P, owned = gemm_rs_ref(A, B, peers, rank, cfg.world)
     assert rel_fro(out.float(), owned) < TOL
@@ -186,6 +192,7 @@ def test_gemm_rs_equal_partials_known_answer(dev):
     peers = own.to(torch.bfloat16).unsqueeze(0).repeat(world - 1, 1, 1).contiguous()
     work = torch.zeros((M, N), dtype=torch.bfloat16, device=dev)
     out = torch.zeros((rows, N), dtype=torch.bfloat16, device=dev)
-    ops.gemm_rs(A.to(dev), B.to(dev), work, out, None, peers.to(dev), world, rank, None, None, epoch=1, gated=False)
+    ops.gemm_rs(A.to(dev), B.to(dev), work, out, None, peers.to(dev), world, rank, None, None, epoch=1, gated=False,
+                num_producers=0)
     torch.cuda.synchronize()
     assert torch.equal(out.cpu(), (own * world).to(torch.bfloat16))

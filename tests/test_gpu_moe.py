@@ -34,14 +34,15 @@ def test_permute_bit_exact(dev):
     assert torch.equal(post.cpu(), om.permute_ref(tokens, idx["pull_indices"]))
 
 
-@pytest.mark.parametrize("use_rb", [True, False])
-def test_grouped_gemm1(dev, use_rb):
-    _say(f"moe grouped gemm1 use_rb={use_rb}")
+@pytest.mark.parametrize("use_rb,skip_pad", [(True, False), (False, False), (True, True)])
+def test_grouped_gemm1(dev, use_rb, skip_pad):
+    _say(f"moe grouped gemm1 use_rb={use_rb} skip_pad={skip_pad}")
     tokens, ids, gates, w1, w2, idx, d = _setup(dev)
     post = om.permute_ref(tokens, idx["pull_indices"])
-    out = torch.empty((idx["R_pad"], 2 * SMALL.I), dtype=torch.bfloat16, device=dev)
+    out = torch.full((idx["R_pad"], 2 * SMALL.I), 3.0, dtype=torch.bfloat16, device=dev)
     ops.moe_grouped_gemm(post.to(dev), w1.to(dev), out, rb_expert=d["rb_expert"] if use_rb else None,
-                         padded_tokens_per_expert=None if use_rb else d["padded_tokens_per_expert"], mode=0)
+                         padded_tokens_per_expert=None if use_rb else d["padded_tokens_per_expert"], mode=0,
+                         rb_rows=d["rb_rows"] if skip_pad else None)
     torch.cuda.synchronize()
     ref = om.grouped_gemm_ref(post, w1, idx["padded_tokens_per_expert"])
     assert rel_fro(out.float(), ref) < TOL
@@ -72,6 +73,15 @@ def test_combine(dev):
         assert rel_fro(y.float(), ref) < (1e-6 if dtype == torch.float32 else 1e-2)
 
 
+def test_tile_rows_bit_exact(dev):
+    tokens, ids, gates, w1, w2, idx, d = _setup(dev)
+    rb = torch.full((idx["R_pad"] // 128,), -1, dtype=torch.int32, device=dev)
+    ops.moe_tile_rows(d["pull_indices"], rb)
+    torch.cuda.synchronize()
+    assert np.array_equal(rb.cpu().numpy(), idx["rb_rows"])
+    assert np.array_equal(idx["rb_rows"], om.build_indices_np(ids, gates, SMALL.e0, SMALL.n_local)["rb_rows"])
+
+
 def test_invert_slots_bit_exact(dev):
     tokens, ids, gates, w1, w2, idx, d = _setup(dev)
     s2r = torch.full((idx["R"],), -5, dtype=torch.int32, device=dev)
@@ -89,7 +99,7 @@ def test_ffn_combine_end_to_end(dev):
     ye = torch.empty((R_pad, SMALL.H), dtype=torch.bfloat16, device=dev)
     y = torch.empty((SMALL.tokens, SMALL.H), dtype=torch.bfloat16, device=dev)
     ops.moe_ffn_combine(tokens.to(dev), d["pull_indices"], d["row_weight"], d["owner_offset"], d["slot_to_row"],
-                        w1.to(dev), w2.to(dev), post, act, ye, y, rb_expert=d["rb_expert"])
+                        w1.to(dev), w2.to(dev), post, act, ye, y, rb_expert=d["rb_expert"], rb_rows=d["rb_rows"])
     torch.cuda.synchronize()
     post_ref = om.permute_ref(tokens, idx["pull_indices"])
     assert torch.equal(post.cpu(), post_ref)

@@ -89,6 +89,7 @@ def test_index_restatements_agree(seed, T, E, k, ep, rank):
         assert np.array_equal(a, np.asarray(npv[key])), key
         assert np.array_equal(a, np.asarray(cv[key])), key
     assert np.array_equal(np.asarray(py["rb_expert"]), npv["rb_expert"])
+    assert np.array_equal(np.asarray(py["rb_rows"]), npv["rb_rows"])
     assert np.array_equal(np.asarray(py["local_rb_per_expert"]), npv["local_rb_per_expert"])
 
 
