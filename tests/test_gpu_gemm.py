@@ -122,6 +122,30 @@ def test_ag_gemm_epochs_and_orders(dev):
     assert all(torch.equal(outs[0], o) for o in outs[1:])
 
 
+@pytest.mark.parametrize("num_cus,K", [(4, 512), (8, 1024), (3, 2048), (0, 512)])
+def test_ag_gemm_streamed_staging(dev, num_cus, K):
+    """Streamed staging (pieces copied inside the K loops, several rounds of
+    tiles per workgroup when the grid is capped): staged bytes and flags
+    exact, result bit-equal to the ungated GEMM, over several epochs."""
+    _say(f"ag_gemm streamed num_cus={num_cus} K={K}")
+    cfg, A, B, order = _ag_case(dev, K=K)
+    Ad, Bd = A.to(dev), B.to(dev)
+    flags = torch.zeros(cfg.M // 128, dtype=torch.int32, device=dev)
+    counters = torch.zeros_like(flags)
+    C_ref = torch.empty((cfg.M, cfg.N), dtype=torch.bfloat16, device=dev)
+    ops.ag_gemm(None, Ad, Bd, C_ref, None, None, epoch=1, gated=False, num_producers=0)
+    for epoch in (1, 2, 4):
+        A_full = torch.zeros_like(Ad)
+        C = torch.empty_like(C_ref)
+        ops.ag_gemm(Ad, A_full, Bd, C, flags, order.to(dev), epoch=epoch, num_producers=-2, num_cus=num_cus,
+                    stage_counters=counters)
+        torch.cuda.synchronize()
+        assert torch.equal(A_full.cpu(), A)
+        assert (flags.cpu() == epoch).all()
+        assert torch.equal(C.cpu(), C_ref.cpu())
+    assert rel_fro(C_ref.float(), ag_gemm_ref(A, B)) < TOL
+
+
 def test_ag_gemm_preset_flags(dev):
     """Flags published by someone else (no producer role in the launch)."""
     cfg, A, B, order = _ag_case(dev)
@@ -149,10 +173,11 @@ def test_ag_gemm_bounded_wait_reports_timeout(dev):
     assert rel_fro(C[:half].float(), gemm_ref(A[:half], B)) < TOL
 
 
-@pytest.mark.parametrize("rank,producers", [(0, 4), (3, 8), (7, 0), (5, -1)])
-def test_gemm_rs_vs_oracle(dev, rank, producers):
-    _say(f"gemm_rs rank={rank} producers={producers}")
-    cfg = wl.RsCfg(world=8, rank=rank, M=2048, K=256, N=512)
+@pytest.mark.parametrize("rank,producers,num_cus,K", [(0, 4, 0, 256), (3, 8, 0, 256), (7, 0, 0, 256), (5, -1, 0, 256),
+                                                     (2, -2, 4, 1024), (6, -2, 0, 256), (1, -2, 5, 2048)])
+def test_gemm_rs_vs_oracle(dev, rank, producers, num_cus, K):
+    _say(f"gemm_rs rank={rank} producers={producers} num_cus={num_cus} K={K}")
+    cfg = wl.RsCfg(world=8, rank=rank, M=2048, K=K, N=512)
     A, B, peers, order = wl.rs_inputs(cfg)
     rows = cfg.M // cfg.world
     Ad, Bd = A.to(dev), B.to(dev)
@@ -167,7 +192,7 @@ def test_gemm_rs_vs_oracle(dev, rank, producers):
         flags = torch.full((nfl,), 9, dtype=torch.int32, device=dev)
     counters = torch.zeros(nfl, dtype=torch.int32, device=dev)
     ops.gemm_rs(Ad, Bd, work, out, peers.to(dev), recv, cfg.world, rank, flags, torch.from_numpy(order).to(dev),
-                epoch=9, num_producers=producers, stage_counters=counters)
+                epoch=9, num_producers=producers, stage_counters=counters, num_cus=num_cus)
     torch.cuda.synchronize()
     P, owned = gemm_rs_ref(A, B, peers, rank, cfg.world)
     assert rel_fro(out.float(), owned) < TOL
