@@ -70,11 +70,7 @@ int mk_gemm(const mk_gemm_args* args, void* stream);
  *                            copies its share of 128 KB pieces (in stage
  *                            order), counting pieces per tile in
  *                            stage_counters; the workgroup that completes a
- *                            tile publishes its flag; then all compute
- *   gated, producers == -2 : streamed staging — pieces are copied inside
- *                            the compute K loops, each one round before the
- *                            tiles that read it (pieces needed by the first
- *                            round are copied first); same counters/flags */
+ *                            tile publishes its flag; then all compute    */
 typedef struct mk_ag_gemm_args {
   const void* A_shards;  /* bf16 [M, K]: shards stacked in rank order (source) */
   void* A_full;          /* bf16 [M, K]: gathered A (destination / GEMM input) */

@@ -76,15 +76,6 @@ void set_grid(mk::GemmKParams& p, int total, int n_prod, int ntiles) {
   p.xcd_remap = (p.n_cons % 8 == 0 && p.n_prod % 8 == 0) ? 1 : 0;
 }
 
-// Streamed staging capacity: pieces (128 rows x st_cols/16 bf16 = st_cols/64
-// KB) one workgroup can copy inside one K loop of K/32 stages, four 1 KB
-// units per stage after the ring's lead-in (ring depth 4 + 2).
-int stream_cap(int K, int64_t st_cols) {
-  const int x_cap = K / 32 - 2 - 4;
-  const int64_t upp = st_cols / 64;
-  return x_cap > 0 && upp > 0 ? (int)((4 * (int64_t)x_cap) / upp) : 0;
-}
-
 int check_gemm_shape(int64_t M, int64_t N, int64_t K, int bm) {
   if (M <= 0 || N <= 0 || K <= 0) return fail(MK_ESHAPE, "M, N, K must be positive (got %lld, %lld, %lld)",
                                               (long long)M, (long long)N, (long long)K);
@@ -161,13 +152,10 @@ int mk_ag_gemm(const mk_ag_gemm_args* a, void* stream) {
     if (nflags + a->M / bm > 8192)
       return fail(MK_ESHAPE, "mk_ag_gemm: too many flags for the schedule scratch");
   }
-  if (a->num_producers < -2) return fail(MK_EINVAL, "mk_ag_gemm: num_producers must be >= -2");
+  if (a->num_producers < -1) return fail(MK_EINVAL, "mk_ag_gemm: num_producers must be >= -1");
   if (a->gated && a->num_producers != 0 && !a->A_shards)
     return fail(MK_EINVAL, "mk_ag_gemm: staging needs A_shards");
-  const bool coop = a->gated && a->num_producers < 0;
-  const bool streamed = a->gated && a->num_producers == -2;
-  if (streamed && (nflags > mk::kMaxStageBlocks || a->K % 64))
-    return fail(MK_ESHAPE, "mk_ag_gemm: streamed staging needs M/128 <= %d and K %% 64 == 0", mk::kMaxStageBlocks);
+  const bool coop = a->gated && a->num_producers == -1;
   if (coop && !a->stage_counters) return fail(MK_EINVAL, "mk_ag_gemm: cooperative staging needs stage_counters");
   const int total = a->num_cus > 0 ? a->num_cus : d.cus;
   const int n_prod = (a->gated && a->num_producers > 0) ? a->num_producers : 0;
@@ -197,9 +185,8 @@ int mk_ag_gemm(const mk_ag_gemm_args* a, void* stream) {
       p.st_order = a->stage_order;
       p.st_flags = a->flags;
       p.st_counters = a->stage_counters;
-      p.st_coop = streamed ? 2 : (coop ? 1 : 0);
+      p.st_coop = coop ? 1 : 0;
       p.st_batch = 8;
-      p.st_cap = stream_cap(p.K, a->K);
     }
   }
   hipError_t e = mk::launch_gemm(p, bm, mk::kEpiStore, static_cast<hipStream_t>(stream));
@@ -220,12 +207,8 @@ int mk_gemm_rs(const mk_gemm_rs_args* a, void* stream) {
   if (npeers > 0 && !a->peer_recv) return fail(MK_EINVAL, "mk_gemm_rs: peer_recv is null");
   const int own_rows = (int)(a->M / a->world);
   const int total = a->num_cus > 0 ? a->num_cus : d.cus;
-  if (a->num_producers < -2) return fail(MK_EINVAL, "mk_gemm_rs: num_producers must be >= -2");
-  const bool coop = a->gated && npeers > 0 && a->num_producers < 0;
-  const bool streamed = coop && a->num_producers == -2;
-  if (streamed && (npeers * (a->M / a->world) / 128 > mk::kMaxStageBlocks || a->N % 64))
-    return fail(MK_ESHAPE, "mk_gemm_rs: streamed staging needs at most %d staged blocks and N %% 64 == 0",
-                mk::kMaxStageBlocks);
+  if (a->num_producers < -1) return fail(MK_EINVAL, "mk_gemm_rs: num_producers must be >= -1");
+  const bool coop = a->gated && npeers > 0 && a->num_producers == -1;
   const int n_prod = (a->gated && npeers > 0 && a->num_producers > 0) ? a->num_producers : 0;
   if (a->gated && npeers > 0) {
     if (!a->flags) return fail(MK_EINVAL, "mk_gemm_rs: gated launch needs flags");
@@ -263,9 +246,8 @@ int mk_gemm_rs(const mk_gemm_rs_args* a, void* stream) {
       p.st_order = a->stage_order;
       p.st_flags = a->flags;
       p.st_counters = a->stage_counters;
-      p.st_coop = streamed ? 2 : (coop ? 1 : 0);
+      p.st_coop = coop ? 1 : 0;
       p.st_batch = 8;
-      p.st_cap = stream_cap(p.K, a->N);
     }
   }
   hipError_t e = mk::launch_gemm(p, bm, mk::kEpiReduce, static_cast<hipStream_t>(stream));

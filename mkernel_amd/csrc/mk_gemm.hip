@@ -54,12 +54,6 @@ struct Cfg {
   static constexpr int A_INST = A_BYTES / 1024 / WAVES_;    // DMA instructions per wave per stage
   static constexpr int B_INST = B_BYTES / 1024 / WAVES_;
   static constexpr int LOADS = A_INST + B_INST;             // vmcnt per stage
-  // Streamed staging: COPY_WAVES waves each move one 1 KB unit per K stage
-  // through a ring of COPY_SLOTS LDS slots placed after the operand ring.
-  static constexpr int COPY_WAVES = 4;
-  static constexpr int COPY_SLOTS = S + 2;
-  static constexpr uint32_t COPY_OFF = S * STAGE;
-  static constexpr uint32_t COPY_BYTES = COPY_SLOTS * COPY_WAVES * 1024;
   static_assert(A_INST >= 1 && B_INST >= 1, "tile too small for the wave count");
   static_assert(FM >= 1 && FN >= 2 && FN % 2 == 0, "wave tile");
 };
@@ -129,130 +123,57 @@ __device__ void producer_role(const GemmKParams& p, int pid) {
   }
 }
 
-// Staging pieces: block b (a 128-row block of the staged data) is split into
-// kPieces contiguous pieces.  A piece is copied with nontemporal 16-byte
-// loads/stores; every finished piece bumps its block's counter and the
-// workgroup whose increment completes the block publishes the block's flag.
-// Counters are never reset: completion is detected modulo kPieces.
+// Cooperative staging: every compute workgroup copies its share of the
+// staging pieces (kPieces per 128-row block, taken in stage order so the
+// earliest-needed blocks complete first) before it starts computing.  Each
+// finished piece bumps its block's counter; the workgroup whose increment
+// completes the block publishes the block's flag.  Counters are never reset:
+// completion is detected modulo kPieces.
 template <int NT>
-__device__ __forceinline__ void copy_piece(const GemmKParams& p, int b, int piece) {
+__device__ void coop_stage(const GemmKParams& p, int cid) {
   const int64_t block_elems = (int64_t)kFlagRows * p.st_cols;
   const int64_t piece_vec = block_elems / 8 / kPieces;  // 16-byte units per piece
-  constexpr int U = 16;
-  const u32x4_t* src = reinterpret_cast<const u32x4_t*>(p.st_src + (int64_t)b * block_elems) + piece * piece_vec;
-  u32x4_t* dst = reinterpret_cast<u32x4_t*>(p.st_dst + (int64_t)b * block_elems) + piece * piece_vec;
-  int64_t base = threadIdx.x;
-  for (; base + (int64_t)(U - 1) * NT < piece_vec; base += (int64_t)U * NT) {
-    u32x4_t v[U];
-#pragma unroll
-    for (int u = 0; u < U; ++u) v[u] = __builtin_nontemporal_load(src + base + u * NT);
-#pragma unroll
-    for (int u = 0; u < U; ++u) __builtin_nontemporal_store(v[u], dst + base + u * NT);
-  }
-  for (; base < piece_vec; base += NT) __builtin_nontemporal_store(__builtin_nontemporal_load(src + base), dst + base);
-}
-
-// Count a piece of block b as done (thread 0, after an agent-scope release
-// that covers the piece's stores) and publish the block when complete.
-__device__ __forceinline__ void count_piece(const GemmKParams& p, int b) {
-  const uint32_t old = __hip_atomic_fetch_add(p.st_counters + b, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  if (old % kPieces == kPieces - 1) {
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-    publish_flag(p.st_flags + b, p.epoch);
-  }
-}
-
-// Copy every piece owner(b, piece) assigns to this workgroup, in stage order
-// (earliest-needed blocks first).  Releases are batched: the first piece
-// alone, then p.st_batch pieces per barrier + agent-scope release (each
-// release is an L2 write-back, so fewer is cheaper).
-template <int NT, class Owned>
-__device__ void stage_pieces(const GemmKParams& p, Owned owned) {
   const int total = p.st_nblocks * kPieces;
-  int batch = 1;
-  int bs[8];
-  int n = 0;
-  for (int q = 0; q < total; ++q) {
+  constexpr int U = 16;
+  auto copy_piece = [&](int q) {
     const int pos = q / kPieces, piece = q % kPieces;
     const int b = p.st_order ? p.st_order[pos] : pos;
-    if (!owned(b, piece, q)) continue;
-    copy_piece<NT>(p, b, piece);
-    bs[n++] = b;
-    if (n == batch) {
-      __syncthreads();
-      if (threadIdx.x == 0) {
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-        for (int i = 0; i < n; ++i) count_piece(p, bs[i]);
-      }
-      n = 0;
-      batch = p.st_batch;
+    const u32x4_t* src = reinterpret_cast<const u32x4_t*>(p.st_src + (int64_t)b * block_elems) + piece * piece_vec;
+    u32x4_t* dst = reinterpret_cast<u32x4_t*>(p.st_dst + (int64_t)b * block_elems) + piece * piece_vec;
+    int64_t base = threadIdx.x;
+    for (; base + (int64_t)(U - 1) * NT < piece_vec; base += (int64_t)U * NT) {
+      u32x4_t v[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) v[u] = __builtin_nontemporal_load(src + base + u * NT);
+#pragma unroll
+      for (int u = 0; u < U; ++u) __builtin_nontemporal_store(v[u], dst + base + u * NT);
     }
-  }
-  if (n) {
+    for (; base < piece_vec; base += NT) __builtin_nontemporal_store(__builtin_nontemporal_load(src + base), dst + base);
+    return b;
+  };
+  auto count_piece = [&](int b) {
+    const uint32_t old = __hip_atomic_fetch_add(p.st_counters + b, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (old % kPieces == kPieces - 1) {
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+      publish_flag(p.st_flags + b, p.epoch);
+    }
+  };
+  // Pieces are released in batches of p.st_batch: copy the batch, one
+  // barrier, one agent-scope release (an L2 write-back), then count the
+  // batch's pieces.  Fewer releases cost fewer serialised write-backs; the
+  // first batch is a single piece so the earliest blocks complete early.
+  int q = cid, batch = 1;
+  while (q < total) {
+    int bs[8];
+    int n = 0;
+    for (; n < batch && q < total; ++n, q += p.n_cons) bs[n] = copy_piece(q);
     __syncthreads();
     if (threadIdx.x == 0) {
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-      for (int i = 0; i < n; ++i) count_piece(p, bs[i]);
+      for (int i = 0; i < n; ++i) count_piece(bs[i]);
     }
+    batch = p.st_batch;
   }
-}
-
-// Streamed-staging plan, identical in every workgroup.  For each staged block:
-//   need[b] = round (tile index / n_cons) of the first tile that reads it,
-//             from the tile schedule (grouped order over the row permutation);
-//   jb[b]   = rank of b among the blocks of the same need round, by stage
-//             position.
-// Piece (b, i) gets j = jb[b]*kPieces + i, workgroup j % n_cons, and round
-// need[b] - 1 - j / (st_cap * n_cons): copied during that round's tile (or,
-// for rounds < 0, before any compute).
-struct StreamPlan {
-  short need[kMaxStageBlocks];
-  short jb[kMaxStageBlocks];
-  int list[kMaxTilePieces];
-  int nlist;
-};
-
-template <int BM, int EPI>
-__device__ __forceinline__ int staged_block_row0(const GemmKParams& p, int b) {
-  if constexpr (EPI == kEpiReduce) return p.rs_own_row0 + (b % (p.rs_own_rows / kFlagRows)) * kFlagRows;
-  else return b * kFlagRows;
-}
-
-template <int BM, int EPI, int NT>
-__device__ void build_stream_plan(const GemmKParams& p, const int* row_perm, int* scratch, StreamPlan& sp) {
-  const int tid = threadIdx.x;
-  const int nb = p.st_nblocks;
-  int* pos = scratch;            // [nb]  block -> stage position
-  int* inv = scratch + nb;       // [tiles_m] row tile -> rank in the schedule
-  for (int i = tid; i < nb; i += NT) {
-    const int b = p.st_order ? p.st_order[i] : i;
-    if ((unsigned)b < (unsigned)nb) pos[b] = i;
-  }
-  for (int i = tid; i < p.tiles_m; i += NT) inv[row_perm ? row_perm[i] : i] = i;
-  __syncthreads();
-  const int group = p.group_m * p.tiles_n;
-  for (int b = tid; b < nb; b += NT) {
-    const int q = inv[staged_block_row0<BM, EPI>(p, b) / BM];
-    const int g = q / p.group_m;
-    const int t_first = g * group + (q - g * p.group_m);  // its tile with tn = 0
-    sp.need[b] = (short)(t_first / p.n_cons);
-  }
-  __syncthreads();
-  for (int b = tid; b < nb; b += NT) {
-    int r = 0;
-    for (int c = 0; c < nb; ++c) r += (sp.need[c] == sp.need[b]) && (pos[c] < pos[b]);
-    sp.jb[b] = (short)r;
-  }
-  __syncthreads();
-}
-
-// Round and workgroup of piece (b, i) under the plan; round < 0: prologue.
-__device__ __forceinline__ void piece_slot(const GemmKParams& p, const StreamPlan& sp, int b, int i, int& round,
-                                           int& wg) {
-  const int j = sp.jb[b] * kPieces + i;
-  const int per_round = p.st_cap * p.n_cons;
-  round = per_round > 0 ? sp.need[b] - 1 - j / per_round : -1;
-  wg = j % p.n_cons;
 }
 
 // ---------------------------------------------------------------------------
@@ -380,9 +301,9 @@ __device__ __forceinline__ u32x4_t make_rsrc_v(const void* base, uint32_t bytes)
 // with wait_stage (vmcnt) followed by a workgroup barrier.
 // The compiler's hazard pass does not look inside inline asm, so the wait
 // states are written here: a VMEM instruction that reads an SGPR written by a
-// VALU instruction (v_readlane / v_readfirstlane, e.g. a reloaded spill) needs
-// 5 wait states, and an LDS DMA after an SALU write of M0 needs 1.  Without
-// them the load can use a stale rsrc / soffset and fetch the wrong bytes.
+// VALU instruction (v_readlane / v_readfirstlane, e.g. a reloaded SGPR spill)
+// needs 5 wait states, and an LDS DMA after an SALU write of M0 needs 1.
+// Without them the load can use a stale rsrc / soffset and fetch wrong bytes.
 __device__ __forceinline__ void dma16(u32x4_t r, uint32_t lds_addr, uint32_t voff, uint32_t soff) {
   asm volatile("s_mov_b32 m0, %0\n\ts_nop 4\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
                :
@@ -402,7 +323,7 @@ __device__ __forceinline__ void dma16x2(u32x4_t r, uint32_t lds0, uint32_t lds1,
       : "memory", "m0");
 }
 
-// n DMAs of consecutive 1 KB LDS blocks starting at lds, paired where possible.
+// N DMAs into consecutive 1 KB LDS blocks starting at lds, paired.
 template <int N>
 __device__ __forceinline__ void dma16_run(u32x4_t r, uint32_t lds, const uint32_t (&voff)[N], uint32_t soff) {
 #pragma unroll
@@ -430,38 +351,6 @@ __device__ __forceinline__ void wait_stage(int pending) {
   wait_vm<0>();
 }
 
-// s_waitcnt vmcnt(n) for a run-time n (clamped to 63).
-template <int N>
-__device__ __forceinline__ void wait_vm_ladder(int n) {
-  if constexpr (N < 63) {
-    if (n <= N) { wait_vm<N>(); return; }
-    wait_vm_ladder<N + 1>(n);
-  } else {
-    wait_vm<63>();
-  }
-}
-__device__ __forceinline__ void wait_vm_dyn(int n) {
-  // Binary split keeps the scalar branch chain short.
-  if (n < 16) {
-    if (n < 8) wait_vm_ladder<0>(n);
-    else wait_vm_ladder<8>(n);
-  } else if (n < 32) {
-    wait_vm_ladder<16>(n);
-  } else {
-    wait_vm_ladder<32>(n);
-  }
-}
-
-// Set lane `lane` of a per-wave vector to a scalar value.
-__device__ __forceinline__ uint32_t writelane(uint32_t vec, int val, int lane) {
-  return ((int)(threadIdx.x & 63) == lane) ? (uint32_t)val : vec;
-}
-
-__device__ __forceinline__ void dma_store16(u32x4_t r, u32x4_t v, uint32_t voff) {
-  // s_nop 4: VALU-written SGPR -> VMEM read hazard (see dma16).
-  asm volatile("s_nop 4\n\tbuffer_store_dwordx4 %0, %1, %2, 0 offen" : : "v"(v), "v"(voff), "s"(r) : "memory");
-}
-
 __device__ __forceinline__ bf16x4_t lds_tr4(const char* p) {
   return __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
       (__attribute__((address_space(3))) bf16x4_t*)((__attribute__((address_space(3))) char*)(p)));
@@ -470,8 +359,8 @@ __device__ __forceinline__ bf16x4_t lds_tr4(const char* p) {
 // ---------------------------------------------------------------------------
 // Compute role
 // ---------------------------------------------------------------------------
-template <class C, int EPI, bool STREAM>
-__device__ void compute_role(const GemmKParams& p, int cons_id, char* smem, const int* row_perm, StreamPlan* sp) {
+template <class C, int EPI>
+__device__ void compute_role(const GemmKParams& p, int cons_id, char* smem, const int* row_perm) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
@@ -503,26 +392,7 @@ __device__ void compute_role(const GemmKParams& p, int cons_id, char* smem, cons
   const uint32_t lds_base = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)smem;
   const uint32_t wave_u = __builtin_amdgcn_readfirstlane(wave);
 
-  // Streamed staging: staged pieces move through the copy slots during the K
-  // loop (copy waves 0..3, one 1 KB unit per wave per stage).
-  const int64_t st_block_bytes = (int64_t)kFlagRows * p.st_cols * 2;
-  const int st_piece_bytes = (int)(st_block_bytes / kPieces);
-  const int st_upp = st_piece_bytes / 1024;  // 1 KB units per piece
-  u32x4_t rS, rD;
-  const bool copy_wave = STREAM && wave_u < (uint32_t)C::COPY_WAVES;
-  if constexpr (STREAM) {
-    rS = make_rsrc_v(p.st_src, (uint32_t)(p.st_nblocks * st_block_bytes));
-    rD = make_rsrc_v(p.st_dst, (uint32_t)(p.st_nblocks * st_block_bytes));
-    // Pieces nobody can copy inside a K loop are staged before any compute.
-    stage_pieces<C::NT>(p, [&](int b, int i, int) {
-      int r, wg;
-      piece_slot(p, *sp, b, i, r, wg);
-      return r < 0 && wg == cons_id;
-    });
-  }
-  int round = 0;
-
-  for (int t = cons_id; t < ntiles; t += p.n_cons, ++round) {
+  for (int t = cons_id; t < ntiles; t += p.n_cons) {
     int tm, tn;
     decode_grouped(t, p.tiles_m, p.tiles_n, p.group_m, tm, tn);
     if (row_perm) tm = row_perm[tm];
@@ -555,31 +425,6 @@ __device__ void compute_role(const GemmKParams& p, int cons_id, char* smem, cons
       const int real = __builtin_amdgcn_readfirstlane(p.rb_rows[tm]) - wm * C::WTM;
       fm_active = __builtin_amdgcn_readfirstlane(min(max((real + 31) / 32, 0), C::FM));
     }
-
-    // This tile's share of the streamed staging.
-    int nlist = 0, nin = 0, x_cap = 0, units = 0;
-    if constexpr (STREAM) {
-      if (tid == 0) sp->nlist = 0;
-      __syncthreads();
-      for (int q = tid; q < p.st_nblocks * kPieces; q += C::NT) {
-        int r, wg;
-        piece_slot(p, *sp, q / kPieces, q % kPieces, r, wg);
-        if (r == round && wg == cons_id) {
-          const int idx = atomicAdd(&sp->nlist, 1);
-          if (idx < kMaxTilePieces) sp->list[idx] = q;
-        }
-      }
-      __syncthreads();
-      nlist = __builtin_amdgcn_readfirstlane(min(sp->nlist, kMaxTilePieces));
-      x_cap = max(nk - 2 - C::S, 0);                             // K stages that can start a copy
-      nin = min(nlist, (C::COPY_WAVES * x_cap) / max(st_upp, 1)); // whole pieces copied in the loop
-      units = nin * st_upp;
-    }
-    // Byte offset (within the staged buffers) of 1 KB copy unit u.
-    auto unit_off = [&](int u) -> uint32_t {
-      const int q = sp->list[u / st_upp];
-      return (uint32_t)((q / kPieces) * st_block_bytes + (q % kPieces) * st_piece_bytes + (u % st_upp) * 1024);
-    };
 
     // Flag gate on the A rows of this tile (AllGather consumer side).
     if (p.a_flags) {
@@ -649,22 +494,10 @@ __device__ void compute_role(const GemmKParams& p, int cons_id, char* smem, cons
     };
 
     // Prologue: fill the whole ring, wait for stage 0, read its kk = 0.
-    // In streaming mode vmcnt is accounted at run time: seq counts this
-    // wave's vector-memory instructions, mark[s % 8] is seq just after stage
-    // s's DMA, so "stage s landed" is vmcnt <= seq - mark[s % 8].
-    int seq = 0;
-    uint32_t mark = 0;  // one lane per ring position (v_writelane / v_readlane)
 #pragma unroll
-    for (int s2 = 0; s2 < C::S; ++s2)
-      if (s2 < nk) {
-        issue(s2);
-        if constexpr (STREAM) {
-          seq += C::LOADS;
-          mark = writelane(mark, seq, s2 & 7);
-        }
-      }
-    if constexpr (STREAM) wait_vm_dyn(seq - __builtin_amdgcn_readlane(mark, 0));
-    else wait_stage<C::S + 1, C::LOADS>(min(C::S - 1, nk - 1));
+    for (int s = 0; s < C::S; ++s)
+      if (s < nk) issue(s);
+    wait_stage<C::S + 1, C::LOADS>(min(C::S - 1, nk - 1));
     __syncthreads();
     read_frags(0, 0);
 
@@ -674,66 +507,19 @@ __device__ void compute_role(const GemmKParams& p, int cons_id, char* smem, cons
     // so the barrier and the LDS reads overlap MFMAs already issued.  The
     // last stage is peeled off: with no branch around the barrier block the
     // compiler's LDS wait counts stay exact, and the kk=1 MFMAs do not wait
-    // for the next stage's reads.  Streaming adds, per copy wave and stage:
-    // copy unit x = kt goes HBM -> copy slot (LDS DMA), and unit
-    // x = kt - S - 1 (landed by now) goes copy slot -> VGPRs -> staged buffer.
+    // for the next stage's reads.
     for (int kt = 0; kt < nk - 1; ++kt) {
       read_frags(kt % C::S, 1);
-      u32x4_t cdata;
-      const int xs = kt - C::S - 1;  // unit stored this stage
-      if constexpr (STREAM) {
-        const int slot = xs >= 0 ? xs % C::COPY_SLOTS : 0;
-        cdata = *reinterpret_cast<const u32x4_t*>(smem + C::COPY_OFF + slot * (C::COPY_WAVES * 1024) +
-                                                  (wave & (C::COPY_WAVES - 1)) * 1024 + lane * 16);
-      }
       mfma(0);
-      if constexpr (STREAM) {
-        wait_vm_dyn(seq - __builtin_amdgcn_readlane(mark, (kt + 1) & 7));
-      } else {
-        wait_stage<C::S + 1, C::LOADS>(min(C::S - 1, nk - 1 - kt) - 1);
-      }
+      wait_stage<C::S + 1, C::LOADS>(min(C::S - 1, nk - 1 - kt) - 1);
       __syncthreads();
-      if (kt + C::S < nk) {
-        issue(kt + C::S);
-        if constexpr (STREAM) {
-          seq += C::LOADS;
-          mark = writelane(mark, seq, (kt + C::S) & 7);
-        }
-      }
-      if constexpr (STREAM) {
-        if (copy_wave) {
-          const int us = xs * C::COPY_WAVES + (int)wave_u;
-          if (xs >= 0 && us < units) {
-            dma_store16(rD, cdata, unit_off(us) + lane * 16);
-            ++seq;
-          }
-          const int ul = kt * C::COPY_WAVES + (int)wave_u;
-          if (kt < x_cap && ul < units) {
-            dma16(rS, lds_base + C::COPY_OFF + (kt % C::COPY_SLOTS) * (C::COPY_WAVES * 1024) + wave_u * 1024,
-                  unit_off(ul) + lane * 16, 0);
-            ++seq;
-          }
-        }
-      }
+      if (kt + C::S < nk) issue(kt + C::S);
       read_frags((kt + 1) % C::S, 0);
       mfma(1);
     }
     read_frags((nk - 1) % C::S, 1);
     mfma(0);
     mfma(1);
-    if constexpr (STREAM) {
-      if (nlist > 0) {
-        // Pieces that did not fit in the K loop, then one release for the
-        // tile's pieces (the barrier waits for every wave's stores).
-        wait_vm<0>();
-        for (int li = nin; li < nlist; ++li) copy_piece<C::NT>(p, sp->list[li] / kPieces, sp->list[li] % kPieces);
-        __syncthreads();
-        if (tid == 0) {
-          __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-          for (int li = 0; li < nlist; ++li) count_piece(p, sp->list[li] / kPieces);
-        }
-      }
-    }
     // Every wave must be done with the ring before the next tile's DMA.
     __syncthreads();
     store_tile<C, EPI>(p, acc, m0, tn, tid);
@@ -792,10 +578,7 @@ __global__ __launch_bounds__(64 * WAVES, 1) void gemm_kernel(GemmKParams p) {
     return;
   }
   int cons = blockIdx.x - p.n_prod;
-  if (p.st_coop == 1) {
-    const int cid = cons;
-    stage_pieces<C::NT>(p, [&](int, int, int q) { return q % p.n_cons == cid; });
-  }
+  if (p.st_coop) coop_stage<C::NT>(p, cons);
   // XCD-aware renumbering: workgroups are dealt round-robin to the 8 XCDs,
   // so give each XCD a contiguous run of consumer ids (hence of tiles, which
   // the grouped order keeps close in A rows / B columns) for L2 reuse.
@@ -805,15 +588,7 @@ __global__ __launch_bounds__(64 * WAVES, 1) void gemm_kernel(GemmKParams p) {
     build_row_perm<BM, C::NT>(p, row_perm, reinterpret_cast<int*>(smem));
     perm = row_perm;
   }
-  if constexpr (BM == 256 && WAVES == 8) {
-    if (p.st_coop == 2) {
-      __shared__ StreamPlan sp;
-      build_stream_plan<BM, EPI, C::NT>(p, perm, reinterpret_cast<int*>(smem), sp);
-      compute_role<C, EPI, true>(p, cons, smem, perm, &sp);
-      return;
-    }
-  }
-  compute_role<C, EPI, false>(p, cons, smem, perm, nullptr);
+  compute_role<C, EPI>(p, cons, smem, perm);
 }
 
 // ---------------------------------------------------------------------------
@@ -822,16 +597,14 @@ __global__ __launch_bounds__(64 * WAVES, 1) void gemm_kernel(GemmKParams p) {
 template <int BM, int WAVES, int EPI>
 static hipError_t launch_t(const GemmKParams& p, hipStream_t stream) {
   using C = Cfg<BM, WAVES>;
-  constexpr uint32_t max_lds = C::LDS_BYTES + ((BM == 256 && WAVES == 8) ? C::COPY_BYTES : 0);
   static bool attr_set = false;  // once per process (one attribute per kernel)
   if (!attr_set) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_kernel<BM, WAVES, EPI>),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, max_lds);
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, C::LDS_BYTES);
     if (e != hipSuccess) return e;
     attr_set = true;
   }
-  const uint32_t lds = C::LDS_BYTES + (p.st_coop == 2 ? C::COPY_BYTES : 0);
-  hipLaunchKernelGGL((gemm_kernel<BM, WAVES, EPI>), dim3(p.n_prod + p.n_cons), dim3(C::NT), lds, stream, p);
+  hipLaunchKernelGGL((gemm_kernel<BM, WAVES, EPI>), dim3(p.n_prod + p.n_cons), dim3(C::NT), C::LDS_BYTES, stream, p);
   return hipGetLastError();
 }
 

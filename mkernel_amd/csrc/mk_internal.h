@@ -10,8 +10,6 @@ enum Epilogue : int { kEpiStore = 0, kEpiSwiGLU = 1, kEpiReduce = 2 };
 enum PermMode : int { kPermNone = 0, kPermArrival = 1, kPermOwnedLast = 2 };
 constexpr int kMaxTilesM = 512;
 constexpr int kPieces = 16;  // cooperative staging: pieces per 128-row block
-constexpr int kMaxStageBlocks = 512;  // streamed staging: blocks the plan can hold
-constexpr int kMaxTilePieces = 256;   // streamed staging: pieces per workgroup per round
 
 struct GemmKParams {
   // operands
@@ -50,10 +48,8 @@ struct GemmKParams {
   const int* st_order;
   uint32_t* st_flags;
   uint32_t* st_counters;    // cooperative staging: pieces completed per block (mod kPieces)
-  int st_coop;              // 1: every workgroup stages its pieces before computing;
-                            // 2: pieces are copied inside the compute K loops
+  int st_coop;              // 1: every workgroup stages its pieces before computing
   int st_batch;             // pieces per release after the first (1..8)
-  int st_cap;               // streamed staging: pieces per workgroup per round
   // flag protocol
   uint32_t epoch;
   uint32_t spin_limit;

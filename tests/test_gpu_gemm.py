@@ -123,11 +123,11 @@ def test_ag_gemm_epochs_and_orders(dev):
 
 
 @pytest.mark.parametrize("num_cus,K", [(4, 512), (8, 1024), (3, 2048), (0, 512)])
-def test_ag_gemm_streamed_staging(dev, num_cus, K):
-    """Streamed staging (pieces copied inside the K loops, several rounds of
-    tiles per workgroup when the grid is capped): staged bytes and flags
+def test_ag_gemm_cooperative_staging_capped_grid(dev, num_cus, K):
+    """Cooperative staging with a capped grid (every workgroup copies many
+    pieces and computes several rounds of tiles): staged bytes and flags
     exact, result bit-equal to the ungated GEMM, over several epochs."""
-    _say(f"ag_gemm streamed num_cus={num_cus} K={K}")
+    _say(f"ag_gemm cooperative num_cus={num_cus} K={K}")
     cfg, A, B, order = _ag_case(dev, K=K)
     Ad, Bd = A.to(dev), B.to(dev)
     flags = torch.zeros(cfg.M // 128, dtype=torch.int32, device=dev)
@@ -137,7 +137,7 @@ def test_ag_gemm_streamed_staging(dev, num_cus, K):
     for epoch in (1, 2, 4):
         A_full = torch.zeros_like(Ad)
         C = torch.empty_like(C_ref)
-        ops.ag_gemm(Ad, A_full, Bd, C, flags, order.to(dev), epoch=epoch, num_producers=-2, num_cus=num_cus,
+        ops.ag_gemm(Ad, A_full, Bd, C, flags, order.to(dev), epoch=epoch, num_producers=-1, num_cus=num_cus,
                     stage_counters=counters)
         torch.cuda.synchronize()
         assert torch.equal(A_full.cpu(), A)
@@ -174,7 +174,7 @@ def test_ag_gemm_bounded_wait_reports_timeout(dev):
 
 
 @pytest.mark.parametrize("rank,producers,num_cus,K", [(0, 4, 0, 256), (3, 8, 0, 256), (7, 0, 0, 256), (5, -1, 0, 256),
-                                                     (2, -2, 4, 1024), (6, -2, 0, 256), (1, -2, 5, 2048)])
+                                                     (2, -1, 4, 1024), (6, -1, 3, 256), (1, -1, 5, 2048)])
 def test_gemm_rs_vs_oracle(dev, rank, producers, num_cus, K):
     _say(f"gemm_rs rank={rank} producers={producers} num_cus={num_cus} K={K}")
     cfg = wl.RsCfg(world=8, rank=rank, M=2048, K=K, N=512)
