@@ -48,6 +48,10 @@ typedef struct mk_gemm_args {
   int32_t num_cus; /* persistent grid size; 0 = every CU of the device */
   int32_t tile_m;  /* 0 = auto, else 128 or 256 */
   int32_t waves;   /* waves per workgroup: 0 = auto, 4 (one per SIMD) or 8 (two per SIMD) */
+  void* split_ws;          /* optional K-split workspace (see mk_query_workspace_bytes);
+                              zero-filled before its first use, left zeroed by every
+                              launch; NULL = no K-split of the tail round */
+  int64_t split_ws_bytes;
 } mk_gemm_args;
 int mk_gemm(const mk_gemm_args* args, void* stream);
 
@@ -86,6 +90,10 @@ typedef struct mk_ag_gemm_args {
   uint32_t spin_limit;          /* polls before a wait gives up; 0 = unbounded */
   uint32_t* error_word;         /* optional device word, bit0 set on timeout */
   uint32_t* stage_counters;     /* [M/128] piece counters for producers == -1; zero once, never reset */
+  void* split_ws;          /* optional K-split workspace (see mk_query_workspace_bytes);
+                              zero-filled before its first use, left zeroed by every
+                              launch; NULL = no K-split of the tail round */
+  int64_t split_ws_bytes;
 } mk_ag_gemm_args;
 int mk_ag_gemm(const mk_ag_gemm_args* args, void* stream);
 
@@ -118,6 +126,10 @@ typedef struct mk_gemm_rs_args {
   uint32_t spin_limit;
   uint32_t* error_word;
   uint32_t* stage_counters;     /* [(world-1) * (M/world)/128] for producers == -1 */
+  void* split_ws;          /* optional K-split workspace (see mk_query_workspace_bytes);
+                              zero-filled before its first use, left zeroed by every
+                              launch; NULL = no K-split of the tail round */
+  int64_t split_ws_bytes;
 } mk_gemm_rs_args;
 int mk_gemm_rs(const mk_gemm_rs_args* args, void* stream);
 
@@ -246,9 +258,16 @@ typedef struct mk_moe_ffn_args {
 int mk_moe_ffn_combine(const mk_moe_ffn_args* args, void* stream);
 
 /* ------------------------------------------------------------------------ */
-/* Scratch sizes.  Every entry point above works on caller buffers only; this
- * reports 0 for all of them and exists so callers can size a workspace the
- * same way for future kernels.  which: 0 gemm, 1 ag, 2 rs, 3 moe. */
+/* K-split workspace size.  When the output tiles do not fill the last round
+ * of the persistent grid (tiles % compute workgroups != 0), the GEMM entry
+ * points split each tile of that tail round along K over 2-4 workgroups;
+ * the parts exchange fp32 partial tiles and ready flags through `split_ws`.
+ * This returns the bytes `split_ws` needs on the current device for any
+ * shape and grid (4 KB of flag words plus one 256x256 fp32 tile per CU); `which`, M,
+ * N and K are accepted for symmetry and do not change the answer.  A
+ * workspace serves one launch at a time: launches that share it must be
+ * ordered (same stream).  No counterpart in the reference, whose tail round
+ * simply idles (src/ag_gemm.cu:265-461). */
 int64_t mk_query_workspace_bytes(int32_t which, int64_t M, int64_t N, int64_t K);
 
 /* Number of compute units of the current device (0 if no device). */
@@ -256,7 +275,7 @@ int32_t mk_device_cu_count(void);
 
 const char* mk_last_error_string(void);
 
-/* ABI version, bumped on any signature change. */
+/* ABI version, bumped on any signature change (2: split_ws fields). */
 int32_t mk_abi_version(void);
 
 #ifdef __cplusplus

@@ -49,7 +49,7 @@ class MkError(RuntimeError):
 class GemmArgs(C.Structure):
     _fields_ = [("A", vp), ("B", vp), ("C", vp), ("M", i64), ("N", i64), ("K", i64),
                 ("lda", i64), ("ldb", i64), ("ldc", i64), ("num_cus", i32), ("tile_m", i32),
-                ("waves", i32)]
+                ("waves", i32), ("split_ws", vp), ("split_ws_bytes", i64)]
 
 
 class AgGemmArgs(C.Structure):
@@ -57,7 +57,7 @@ class AgGemmArgs(C.Structure):
                 ("M", i64), ("N", i64), ("K", i64),
                 ("flags", vp), ("stage_order", vp), ("epoch", u32), ("gated", i32),
                 ("num_producers", i32), ("num_cus", i32), ("spin_limit", u32), ("error_word", vp),
-                ("stage_counters", vp)]
+                ("stage_counters", vp), ("split_ws", vp), ("split_ws_bytes", i64)]
 
 
 class GemmRsArgs(C.Structure):
@@ -65,7 +65,7 @@ class GemmRsArgs(C.Structure):
                 ("peer_recv", vp), ("M", i64), ("N", i64), ("K", i64), ("world", i32), ("rank", i32),
                 ("flags", vp), ("stage_order", vp), ("epoch", u32), ("gated", i32),
                 ("num_producers", i32), ("num_cus", i32), ("spin_limit", u32), ("error_word", vp),
-                ("stage_counters", vp)]
+                ("stage_counters", vp), ("split_ws", vp), ("split_ws_bytes", i64)]
 
 
 class MoeIndex(C.Structure):

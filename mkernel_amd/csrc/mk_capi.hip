@@ -86,13 +86,45 @@ int check_gemm_shape(int64_t M, int64_t N, int64_t K, int bm) {
   return MK_OK;
 }
 
+constexpr int64_t kSplitTileBytes = 256 * 256 * 4;  // one fp32 BM x 256 partial (BM <= 256)
+constexpr int64_t kSplitFlagBytes = 4096;           // flag words at the start of the workspace
+
+int64_t split_ws_bytes(int cus) { return kSplitFlagBytes + (int64_t)cus * kSplitTileBytes; }
+
+// K-split plan for the tail round: with R = tiles % n_cons tiles left for a
+// partial last round, split each of them s = min(4, n_cons / R) ways along
+// K so that R*s workgroups share the round.  The workspace holds the flag
+// words at a fixed offset (so every plan finds them zeroed) followed by
+// R*(s-1) < n_cons <= CUs partial tiles, which split_ws_bytes covers.
+void plan_split(mk::GemmKParams& p, int bm, void* ws, int64_t ws_bytes) {
+  const int ntiles = p.tiles_m * p.tiles_n;
+  const int R = ntiles % p.n_cons;
+  if (!ws || R == 0 || p.waves != 8) return;
+  if (p.perm_mode != mk::kPermNone && ntiles > mk::kMaxSplitListTiles) return;
+  int s = std::min(4, p.n_cons / R);
+  s = std::min(s, (p.K / 32) / 4);  // keep every part at >= 4 K stages
+  if (s < 2) return;
+  const int64_t parts = (int64_t)R * (s - 1);
+  if (parts * 4 > kSplitFlagBytes || kSplitFlagBytes + parts * bm * 256 * 4 > ws_bytes) return;
+  p.sk_flags = static_cast<uint32_t*>(ws);
+  p.sk_ws = reinterpret_cast<float*>(static_cast<char*>(ws) + kSplitFlagBytes);
+  p.sk_full = ntiles - R;
+  p.sk_split = s;
+}
+
+int check_ws(const void* ws, int64_t bytes, const char* fn) {
+  if (ws && (bytes < 0 || (reinterpret_cast<uintptr_t>(ws) & 255u)))
+    return fail(MK_EINVAL, "%s: split_ws must be 256-byte aligned with a non-negative size", fn);
+  return MK_OK;
+}
+
 }  // namespace
 
 extern "C" {
 
 const char* mk_last_error_string(void) { return g_err.c_str(); }
 
-int32_t mk_abi_version(void) { return 1; }
+int32_t mk_abi_version(void) { return 2; }
 
 int32_t mk_device_cu_count(void) {
   DevInfo d;
@@ -102,7 +134,9 @@ int32_t mk_device_cu_count(void) {
 
 int64_t mk_query_workspace_bytes(int32_t which, int64_t M, int64_t N, int64_t K) {
   (void)which; (void)M; (void)N; (void)K;
-  return 0;
+  DevInfo d;
+  if (device_info(&d) != MK_OK) return -1;
+  return split_ws_bytes(d.cus);
 }
 
 int mk_gemm(const mk_gemm_args* a, void* stream) {
@@ -133,6 +167,8 @@ int mk_gemm(const mk_gemm_args* a, void* stream) {
   const int total = a->num_cus > 0 ? a->num_cus : d.cus;
   set_grid(p, total, 0, p.tiles_m * p.tiles_n);
   if (a->waves) p.waves = a->waves;
+  if (int rc = check_ws(a->split_ws, a->split_ws_bytes, "mk_gemm")) return rc;
+  plan_split(p, bm, a->split_ws, a->split_ws_bytes);
   hipError_t e = mk::launch_gemm(p, bm, mk::kEpiStore, static_cast<hipStream_t>(stream));
   return e == hipSuccess ? MK_OK : hip_fail(e, "mk_gemm launch");
 }
@@ -189,6 +225,8 @@ int mk_ag_gemm(const mk_ag_gemm_args* a, void* stream) {
       p.st_batch = 8;
     }
   }
+  if (int rc = check_ws(a->split_ws, a->split_ws_bytes, "mk_ag_gemm")) return rc;
+  plan_split(p, bm, a->split_ws, a->split_ws_bytes);
   hipError_t e = mk::launch_gemm(p, bm, mk::kEpiStore, static_cast<hipStream_t>(stream));
   return e == hipSuccess ? MK_OK : hip_fail(e, "mk_ag_gemm launch");
 }
@@ -250,6 +288,8 @@ int mk_gemm_rs(const mk_gemm_rs_args* a, void* stream) {
       p.st_batch = 8;
     }
   }
+  if (int rc = check_ws(a->split_ws, a->split_ws_bytes, "mk_gemm_rs")) return rc;
+  plan_split(p, bm, a->split_ws, a->split_ws_bytes);
   hipError_t e = mk::launch_gemm(p, bm, mk::kEpiReduce, static_cast<hipStream_t>(stream));
   return e == hipSuccess ? MK_OK : hip_fail(e, "mk_gemm_rs launch");
 }

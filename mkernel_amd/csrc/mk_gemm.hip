@@ -356,18 +356,67 @@ __device__ __forceinline__ bf16x4_t lds_tr4(const char* p) {
       (__attribute__((address_space(3))) bf16x4_t*)((__attribute__((address_space(3))) char*)(p)));
 }
 
+// Partial-sum exchange for K-split tail tiles.  A tile's NT threads hold
+// FM*FN*16 fp32 accumulators each; they go to the workspace as 16-byte
+// units in register order, unit ((i*FN + j)*4 + a)*NT + tid, so writes and
+// reads are fully coalesced and need no layout conversion.  Buffer
+// instructions keep the per-unit offsets in scalar registers (one VGPR of
+// addressing in total), which matters: the accumulators already hold most
+// of the register file.
+template <class C>
+__device__ __forceinline__ void put_partial(float* dst, f32x16 (&acc)[C::FM][C::FN], int tid) {
+  const __amdgpu_buffer_rsrc_t r = make_rsrc(dst, (uint32_t)(C::BM * kBN * 4));
+#pragma unroll
+  for (int i = 0; i < C::FM; ++i)
+#pragma unroll
+    for (int j = 0; j < C::FN; ++j)
+#pragma unroll
+      for (int a = 0; a < 4; ++a) {
+        f32x4 v;
+#pragma unroll
+        for (int b = 0; b < 4; ++b) v[b] = acc[i][j][4 * a + b];
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, v), r, tid * 16,
+                                               ((i * C::FN + j) * 4 + a) * C::NT * 16, 0);
+      }
+}
+
+template <class C>
+__device__ __forceinline__ void add_partial(const float* src, f32x16 (&acc)[C::FM][C::FN], int tid) {
+  const __amdgpu_buffer_rsrc_t r = make_rsrc(src, (uint32_t)(C::BM * kBN * 4));
+#pragma unroll
+  for (int i = 0; i < C::FM; ++i)
+#pragma unroll
+    for (int j = 0; j < C::FN; ++j)
+#pragma unroll
+      for (int a = 0; a < 4; ++a) {
+        const f32x4 v = __builtin_bit_cast(
+            f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, tid * 16, ((i * C::FN + j) * 4 + a) * C::NT * 16, 0));
+#pragma unroll
+        for (int b = 0; b < 4; ++b) acc[i][j][4 * a + b] += v[b];
+      }
+}
+
 // ---------------------------------------------------------------------------
 // Compute role
+//
+// Work of one consumer: the tiles cons_id, cons_id + n_cons, ... below
+// sk_full (whole K each), then, when the tile count leaves a partial last
+// round (sk_split > 1), one K-split unit of a tail tile: consumer u works on
+// tail tile sk_full + u / sk_split, K part u % sk_split.  Parts 1.. write
+// fp32 partials to the workspace and release a flag; part 0 acquires the
+// flags, adds the partials in part order (deterministic) and runs the
+// epilogue.  Every round then keeps all consumers busy.
 // ---------------------------------------------------------------------------
 template <class C, int EPI>
-__device__ void compute_role(const GemmKParams& p, int cons_id, char* smem, const int* row_perm) {
+__device__ void compute_role(const GemmKParams& p, int cons_id, char* smem, const int* row_perm,
+                             const uint16_t* full_list) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
   const int wm = wave / C::WN;
   const int wn = wave % C::WN;
   const int ntiles = p.tiles_m * p.tiles_n;
-  const int nk = p.K / C::BKD;
+  const int nk_all = p.K / C::BKD;
 
   // A operand read: row wm*WTM + ml (+32 i), 16-byte unit 2kk + g.
   const int ml = lane & 31, g = lane >> 5;
@@ -392,10 +441,20 @@ __device__ void compute_role(const GemmKParams& p, int cons_id, char* smem, cons
   const uint32_t lds_base = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)smem;
   const uint32_t wave_u = __builtin_amdgcn_readfirstlane(wave);
 
-  for (int t = cons_id; t < ntiles; t += p.n_cons) {
+  const int full = (p.sk_split > 1) ? p.sk_full : ntiles;
+  const int n_tail_units = (ntiles - full) * (p.sk_split > 1 ? p.sk_split : 0);
+  const int n_full_mine = (full > cons_id) ? (full - cons_id + p.n_cons - 1) / p.n_cons : 0;
+
+  // One output tile (or one K range of it): accumulate A[rows] @ B[:, cols]
+  // over K stages k0 .. k0+nk into acc.  Called from two places (whole
+  // tiles, the K-split unit) so that each call site gets its own register
+  // allocation: the partial exchange of the split unit must not raise the
+  // register pressure of the whole-tile loop.
+  auto tile_body = [&](int t, bool permuted, int k0, int nk, f32x16 (&acc)[C::FM][C::FN], int& m0_out,
+                       int& tn_out) __attribute__((always_inline)) {
     int tm, tn;
     decode_grouped(t, p.tiles_m, p.tiles_n, p.group_m, tm, tn);
-    if (row_perm) tm = row_perm[tm];
+    if (permuted) tm = row_perm[tm];
     // Tile coordinates are wave-uniform; keep them scalar.
     tm = __builtin_amdgcn_readfirstlane(tm);
     tn = __builtin_amdgcn_readfirstlane(tn);
@@ -452,15 +511,15 @@ __device__ void compute_role(const GemmKParams& p, int cons_id, char* smem, cons
       const int c = (lane & 31) ^ (4 * (krow & 3));
       b_src[i] = (uint32_t)(krow * p.ldb * 2 + b_col<C, EPI>(p, tn, c * 8) * 2);
     }
+    // Stage kt of this unit is global K stage k0 + kt, kept in ring slot kt % S.
     auto issue = [&](int kt) {
       const uint32_t st = lds_base + (uint32_t)(kt % C::S) * C::STAGE;
-      const uint32_t ka = (uint32_t)kt * (C::BKD * 2);
-      const uint32_t kb = (uint32_t)kt * (C::BKD * p.ldb * 2);
+      const uint32_t ka = (uint32_t)(k0 + kt) * (C::BKD * 2);
+      const uint32_t kb = (uint32_t)(k0 + kt) * (C::BKD * p.ldb * 2);
       dma16_run<C::A_INST>(rA, st + wave_u * C::A_INST * 1024, a_src, ka);
       dma16_run<C::B_INST>(rB, st + C::A_BYTES + wave_u * C::B_INST * 1024, b_src, kb);
     };
 
-    f32x16 acc[C::FM][C::FN];
 #pragma unroll
     for (int i = 0; i < C::FM; ++i)
 #pragma unroll
@@ -493,37 +552,136 @@ __device__ void compute_role(const GemmKParams& p, int cons_id, char* smem, cons
         }
     };
 
-    // Prologue: fill the whole ring, wait for stage 0, read its kk = 0.
+    if constexpr (C::WAVES == 8) {
+      // Ping-pong schedule.  Waves 0-3 (group X) and 4-7 (group Y) hold one
+      // wave of each SIMD.  Phases are separated by workgroup barriers; in
+      // every phase one group runs a memory step M(j) (all LDS operand reads
+      // of stage j into registers, plus the DMA of stage j+S-1 into the slot
+      // stage j-1 left) while the other runs the compute step C (the stage's
+      // MFMAs from registers), so each SIMD's MFMA pipe is fed by one wave
+      // while its partner loads:
+      //   phase 0:    X M(0)
+      //   phase 2j+1: X C(j)    Y M(j)
+      //   phase 2j+2: X M(j+1)  Y C(j)
+      // Before the barrier that ends phase 2j+1 every wave waits for its own
+      // DMA of stage j+1, so stage j+1 is complete when X reads it.
+      const bool grp_x = wave_u < (uint32_t)(C::WAVES / 2);
+      auto mem_step = [&](int j) {
+        if (j + C::S - 1 < nk) issue(j + C::S - 1);
+        read_frags(j % C::S, 0);
+        read_frags(j % C::S, 1);
+      };
+      auto wait_j = [&](int j) { wait_stage<C::S + 1, C::LOADS>(min(C::S - 2, nk - 1 - j)); };
+      auto bar = [] {
+        __builtin_amdgcn_sched_barrier(0);
+        __syncthreads();
+        __builtin_amdgcn_sched_barrier(0);
+      };
 #pragma unroll
-    for (int s = 0; s < C::S; ++s)
-      if (s < nk) issue(s);
-    wait_stage<C::S + 1, C::LOADS>(min(C::S - 1, nk - 1));
-    __syncthreads();
-    read_frags(0, 0);
-
-    // Steady state for stage kt (ring slot kt % S):
-    //   read kk=1 operands | MFMA kk=0 | wait stage kt+1 + barrier |
-    //   refill the slot with stage kt+S | read stage kt+1 kk=0 | MFMA kk=1
-    // so the barrier and the LDS reads overlap MFMAs already issued.  The
-    // last stage is peeled off: with no branch around the barrier block the
-    // compiler's LDS wait counts stay exact, and the kk=1 MFMAs do not wait
-    // for the next stage's reads.
-    for (int kt = 0; kt < nk - 1; ++kt) {
-      read_frags(kt % C::S, 1);
-      mfma(0);
-      wait_stage<C::S + 1, C::LOADS>(min(C::S - 1, nk - 1 - kt) - 1);
+      for (int s = 0; s < C::S - 1; ++s)
+        if (s < nk) issue(s);
+      wait_j(0);
       __syncthreads();
-      if (kt + C::S < nk) issue(kt + C::S);
-      read_frags((kt + 1) % C::S, 0);
+      // The two groups run separate loops (same barrier count per iteration)
+      // so each keeps a single set of fragment registers live.
+      if (grp_x) {
+        mem_step(0);
+        for (int j = 0; j < nk; ++j) {
+          bar();
+          mfma(0);
+          mfma(1);
+          if (j + 1 < nk) wait_j(j + 1);
+          bar();
+          if (j + 1 < nk) mem_step(j + 1);
+        }
+      } else {
+        for (int j = 0; j < nk; ++j) {
+          bar();
+          mem_step(j);
+          if (j + 1 < nk) wait_j(j + 1);
+          bar();
+          mfma(0);
+          mfma(1);
+        }
+      }
+      // Every wave's last LDS read happened before the loop's final barrier,
+      // so the ring is free for the next unit's prologue.
+    } else {
+      // Lockstep schedule (one wave per SIMD).  Steady state for stage kt:
+      //   read kk=1 operands | MFMA kk=0 | wait stage kt+1 + barrier |
+      //   refill the slot with stage kt+S | read stage kt+1 kk=0 | MFMA kk=1
+      // so the barrier and the LDS reads overlap MFMAs already issued.  The
+      // last stage is peeled off: with no branch around the barrier block
+      // the compiler's LDS wait counts stay exact.
+#pragma unroll
+      for (int s = 0; s < C::S; ++s)
+        if (s < nk) issue(s);
+      wait_stage<C::S + 1, C::LOADS>(min(C::S - 1, nk - 1));
+      __syncthreads();
+      read_frags(0, 0);
+      for (int kt = 0; kt < nk - 1; ++kt) {
+        read_frags(kt % C::S, 1);
+        mfma(0);
+        wait_stage<C::S + 1, C::LOADS>(min(C::S - 1, nk - 1 - kt) - 1);
+        __syncthreads();
+        if (kt + C::S < nk) issue(kt + C::S);
+        read_frags((kt + 1) % C::S, 0);
+        mfma(1);
+      }
+      read_frags((nk - 1) % C::S, 1);
+      mfma(0);
       mfma(1);
+      // Every wave must be done with the ring before the next unit's DMA.
+      __syncthreads();
     }
-    read_frags((nk - 1) % C::S, 1);
-    mfma(0);
-    mfma(1);
-    // Every wave must be done with the ring before the next tile's DMA.
-    __syncthreads();
+
+    m0_out = m0;
+    tn_out = tn;
+  };
+
+  // Whole tiles walk the (possibly arrival-permuted) order, skipping the
+  // split set; the split set is the last tiles of the unpermuted order, so
+  // which tiles are split, and hence every output bit, does not depend on
+  // the arrival order.
+  for (int w = 0; w < n_full_mine; ++w) {
+    int t = cons_id + w * p.n_cons;
+    if (full_list) t = full_list[t];
+    f32x16 acc[C::FM][C::FN];
+    int m0, tn;
+    tile_body(t, row_perm != nullptr, 0, nk_all, acc, m0, tn);
     store_tile<C, EPI>(p, acc, m0, tn, tid);
   }
+  if (cons_id >= n_tail_units) return;
+  // The K-split unit: tail tile full + tail_idx (unpermuted), K part `part`.
+  const int tail_idx = cons_id / p.sk_split;
+  const int part = cons_id % p.sk_split;
+  const int k0 = part * nk_all / p.sk_split;
+  const int nk = (part + 1) * nk_all / p.sk_split - k0;
+  f32x16 acc[C::FM][C::FN];
+  int m0, tn;
+  tile_body(full + tail_idx, false, k0, nk, acc, m0, tn);
+  if (part > 0) {
+    // K-split contributor: publish the partial for part 0 of this tile.
+    const int slot = tail_idx * (p.sk_split - 1) + part - 1;
+    put_partial<C>(p.sk_ws + (int64_t)slot * (C::BM * kBN), acc, tid);
+    __syncthreads();
+    if (tid == 0) publish_flag(p.sk_flags + slot, 1u);
+    return;
+  }
+  {
+    // K-split owner: acquire every contributor's partial, fold in part
+    // order, and clear the flags for the next launch on this workspace.
+    const int slot0 = tail_idx * (p.sk_split - 1);
+    if (tid == 0)
+      for (int q2 = 0; q2 < p.sk_split - 1; ++q2) wait_flag(p.sk_flags + slot0 + q2, 1u, p.spin_limit, p.err);
+    __syncthreads();
+    for (int q2 = 0; q2 < p.sk_split - 1; ++q2)
+      add_partial<C>(p.sk_ws + (int64_t)(slot0 + q2) * (C::BM * kBN), acc, tid);
+    if (tid == 0)
+      for (int q2 = 0; q2 < p.sk_split - 1; ++q2)
+        __hip_atomic_store(p.sk_flags + slot0 + q2, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  store_tile<C, EPI>(p, acc, m0, tn, tid);
 }
 
 // Order of row tiles for a gated consumer: ascending by the stage position at
@@ -568,11 +726,51 @@ __device__ void build_row_perm(const GemmKParams& p, int* row_perm, int* scratch
   __syncthreads();
 }
 
+// Unpermuted tile index of tile (tm, tn): the inverse of decode_grouped.
+__device__ __forceinline__ int encode_grouped(int tm, int tn, int tiles_m, int tiles_n, int group_m) {
+  const int g = tm / group_m;
+  const int first = g * group_m;
+  const int gm = min(tiles_m - first, group_m);
+  return g * group_m * tiles_n + tn * gm + (tm - first);
+}
+
+// Positions of the arrival-permuted order whose tile is not in the split set
+// (tiles sk_full.. of the unpermuted order), in order: full_list[i] is the
+// position of the i-th whole tile.  Each thread takes a contiguous chunk of
+// positions; a block-wide scan of the chunk counts gives the output offsets.
+template <int NT>
+__device__ void build_full_list(const GemmKParams& p, const int* row_perm, uint16_t* full_list, int* scratch) {
+  const int tid = threadIdx.x;
+  const int ntiles = p.tiles_m * p.tiles_n;
+  const int per = (ntiles + NT - 1) / NT;
+  const int lo = min(tid * per, ntiles), hi = min(lo + per, ntiles);
+  auto whole = [&](int pos) {
+    int tm, tn;
+    decode_grouped(pos, p.tiles_m, p.tiles_n, p.group_m, tm, tn);
+    return encode_grouped(row_perm[tm], tn, p.tiles_m, p.tiles_n, p.group_m) < p.sk_full;
+  };
+  int c = 0;
+  for (int i = lo; i < hi; ++i) c += whole(i);
+  scratch[tid] = c;
+  __syncthreads();
+  for (int off = 1; off < NT; off <<= 1) {
+    const int v = tid >= off ? scratch[tid - off] : 0;
+    __syncthreads();
+    scratch[tid] += v;
+    __syncthreads();
+  }
+  int o = scratch[tid] - c;
+  for (int i = lo; i < hi; ++i)
+    if (whole(i)) full_list[o++] = (uint16_t)i;
+  __syncthreads();
+}
+
 template <int BM, int WAVES, int EPI>
 __global__ __launch_bounds__(64 * WAVES, 1) void gemm_kernel(GemmKParams p) {
   using C = Cfg<BM, WAVES>;
   extern __shared__ __attribute__((aligned(16))) char smem[];
   __shared__ int row_perm[kMaxTilesM];
+  __shared__ uint16_t full_list[kMaxSplitListTiles];
   if ((int)blockIdx.x < p.n_prod) {
     producer_role<C::NT>(p, blockIdx.x);
     return;
@@ -588,7 +786,12 @@ __global__ __launch_bounds__(64 * WAVES, 1) void gemm_kernel(GemmKParams p) {
     build_row_perm<BM, C::NT>(p, row_perm, reinterpret_cast<int*>(smem));
     perm = row_perm;
   }
-  compute_role<C, EPI>(p, cons, smem, perm);
+  const uint16_t* flist = nullptr;
+  if (perm && p.sk_split > 1) {
+    build_full_list<C::NT>(p, row_perm, full_list, reinterpret_cast<int*>(smem));
+    flist = full_list;
+  }
+  compute_role<C, EPI>(p, cons, smem, perm, flist);
 }
 
 // ---------------------------------------------------------------------------

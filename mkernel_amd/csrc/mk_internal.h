@@ -9,6 +9,7 @@ namespace mk {
 enum Epilogue : int { kEpiStore = 0, kEpiSwiGLU = 1, kEpiReduce = 2 };
 enum PermMode : int { kPermNone = 0, kPermArrival = 1, kPermOwnedLast = 2 };
 constexpr int kMaxTilesM = 512;
+constexpr int kMaxSplitListTiles = 4096;  // K-split with a permuted tile order: at most this many tiles
 constexpr int kPieces = 16;  // cooperative staging: pieces per 128-row block
 
 struct GemmKParams {
@@ -50,6 +51,11 @@ struct GemmKParams {
   uint32_t* st_counters;    // cooperative staging: pieces completed per block (mod kPieces)
   int st_coop;              // 1: every workgroup stages its pieces before computing
   int st_batch;             // pieces per release after the first (1..8)
+  // K-split of the tail round: tiles >= sk_full are split sk_split ways along
+  // K (sk_split <= 1: no split); partials go through sk_ws with sk_flags
+  float* sk_ws;
+  uint32_t* sk_flags;
+  int sk_full, sk_split;
   // flag protocol
   uint32_t epoch;
   uint32_t spin_limit;

@@ -33,22 +33,52 @@ def cu_count() -> int:
     return int(capi.lib().mk_device_cu_count())
 
 
+_split_ws: dict = {}
+
+
+def split_workspace(device=None) -> torch.Tensor:
+    """The per-device K-split workspace the GEMM entry points use by default:
+    mk_query_workspace_bytes() bytes, zero-filled once (every launch leaves
+    it zeroed).  Launches sharing it must be stream-ordered; pass an explicit
+    ``split_ws`` to run GEMMs concurrently on several streams."""
+    dev = torch.device("cuda", torch.cuda.current_device() if device is None else torch.device(device).index or 0)
+    ws = _split_ws.get(dev)
+    if ws is None:
+        n = int(capi.lib().mk_query_workspace_bytes(0, 0, 0, 0))
+        if n < 0:
+            raise capi.MkError("mk_query_workspace_bytes", n, capi.lib().mk_last_error_string().decode())
+        ws = torch.zeros(n, dtype=torch.uint8, device=dev)
+        _split_ws[dev] = ws
+    return ws
+
+
+def _ws(split_ws, device) -> tuple:
+    """(pointer, bytes) of the K-split workspace: the default one, an explicit
+    tensor, or none at all when split_ws is False."""
+    if split_ws is False:
+        return None, 0
+    ws = split_workspace(device) if split_ws is None or split_ws is True else split_ws
+    return ws.data_ptr(), ws.numel() * ws.element_size()
+
+
 def gemm(A: torch.Tensor, B: torch.Tensor, out: torch.Tensor | None = None, num_cus: int = 0,
-         tile_m: int = 0, waves: int = 0) -> torch.Tensor:
-    """C = A @ B (bf16 in, fp32 accumulate, bf16 out)."""
+         tile_m: int = 0, waves: int = 0, split_ws=None) -> torch.Tensor:
+    """C = A @ B (bf16 in, fp32 accumulate, bf16 out).  split_ws: None = the
+    default per-device K-split workspace, False = no K-split, or a tensor."""
     _bf16(A, "A"); _bf16(B, "B")
     M, K = A.shape
     N = B.shape[1]
     if out is None:
         out = torch.empty((M, N), dtype=torch.bfloat16, device=A.device)
     _bf16(out, "C")
-    capi.call("mk_gemm", GemmArgs(_ptr(A), _ptr(B), _ptr(out), M, N, K, K, N, N, num_cus, tile_m, waves), _stream())
+    capi.call("mk_gemm", GemmArgs(_ptr(A), _ptr(B), _ptr(out), M, N, K, K, N, N, num_cus, tile_m, waves,
+                                  *_ws(split_ws, A.device)), _stream())
     return out
 
 
 def ag_gemm(A_shards, A_full, B, C_out, flags, stage_order, epoch: int, gated: bool = True,
             num_producers: int = -1, num_cus: int = 0, spin_limit: int = 0, error_word=None,
-            stage_counters=None) -> torch.Tensor:
+            stage_counters=None, split_ws=None) -> torch.Tensor:
     """Flag-gated AllGather+GEMM; see include/mk.h mk_ag_gemm.  num_producers
     -1 (default) stages cooperatively and needs stage_counters (int32
     [M/128], zeroed once)."""
@@ -56,21 +86,22 @@ def ag_gemm(A_shards, A_full, B, C_out, flags, stage_order, epoch: int, gated: b
     M, K = A_full.shape
     N = B.shape[1]
     args = AgGemmArgs(_ptr(A_shards), _ptr(A_full), _ptr(B), _ptr(C_out), M, N, K, _ptr(flags), _ptr(stage_order),
-                      epoch, int(gated), num_producers, num_cus, spin_limit, _ptr(error_word), _ptr(stage_counters))
+                      epoch, int(gated), num_producers, num_cus, spin_limit, _ptr(error_word), _ptr(stage_counters),
+                      *_ws(split_ws, A_full.device))
     capi.call("mk_ag_gemm", args, _stream())
     return C_out
 
 
 def gemm_rs(A, B, workspace, output, peer_src, peer_recv, world: int, rank: int, flags, stage_order, epoch: int,
             gated: bool = True, num_producers: int = -1, num_cus: int = 0, spin_limit: int = 0,
-            error_word=None, stage_counters=None) -> torch.Tensor:
+            error_word=None, stage_counters=None, split_ws=None) -> torch.Tensor:
     """GEMM with the reduce-scatter fold in the epilogue; see mk_gemm_rs."""
     _bf16(A, "A"); _bf16(B, "B")
     M, K = A.shape
     N = B.shape[1]
     args = GemmRsArgs(_ptr(A), _ptr(B), _ptr(workspace), _ptr(output), _ptr(peer_src), _ptr(peer_recv), M, N, K,
                       world, rank, _ptr(flags), _ptr(stage_order), epoch, int(gated), num_producers, num_cus,
-                      spin_limit, _ptr(error_word), _ptr(stage_counters))
+                      spin_limit, _ptr(error_word), _ptr(stage_counters), *_ws(split_ws, A.device))
     capi.call("mk_gemm_rs", args, _stream())
     return output
 

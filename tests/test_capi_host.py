@@ -1,6 +1,7 @@
 """CPU-side checks of the C-ABI library: it loads, exports every symbol that
 include/mk.h declares, and its host-side index builder matches the oracle
 bit-exactly.  No device calls."""
+import ctypes as C
 import re
 from pathlib import Path
 
@@ -27,13 +28,39 @@ def test_library_exports_every_declared_symbol():
     L = capi.lib()
     for name in _header_symbols():
         assert hasattr(L, name), name
-    assert L.mk_abi_version() == 1
+    assert L.mk_abi_version() == 2
 
 
-@pytest.mark.parametrize("cls,nfields", [(capi.GemmArgs, 12), (capi.AgGemmArgs, 16), (capi.GemmRsArgs, 20),
-                                         (capi.MoeIndex, 11), (capi.MoeGroupedGemmArgs, 12)])
-def test_struct_layouts(cls, nfields):
-    assert len(cls._fields_) == nfields
+_STRUCTS = {"mk_gemm_args": capi.GemmArgs, "mk_ag_gemm_args": capi.AgGemmArgs, "mk_gemm_rs_args": capi.GemmRsArgs,
+            "mk_moe_index": capi.MoeIndex, "mk_moe_permute_args": capi.MoePermuteArgs,
+            "mk_moe_grouped_gemm_args": capi.MoeGroupedGemmArgs, "mk_moe_combine_args": capi.MoeCombineArgs,
+            "mk_moe_ffn_args": capi.MoeFfnArgs}
+
+
+def test_struct_layouts_match_header(tmp_path):
+    """Every ctypes struct has the size and field offsets the C compiler gives
+    the header's struct (compiled with the host gcc)."""
+    import shutil
+    import subprocess
+    cc = shutil.which("gcc") or shutil.which("cc")
+    if cc is None:
+        pytest.skip("no host C compiler")
+    lines = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{ROOT / "include" / "mk.h"}"', "int main(void) {"]
+    for cname, cls in _STRUCTS.items():
+        lines.append(f'  printf("{cname} size %zu\\n", sizeof({cname}));')
+        for f, _ in cls._fields_:
+            lines.append(f'  printf("{cname} {f} %zu\\n", offsetof({cname}, {f}));')
+    lines.append("  return 0; }")
+    src = tmp_path / "layout.c"
+    src.write_text("\n".join(lines))
+    exe = tmp_path / "layout"
+    subprocess.run([cc, str(src), "-o", str(exe)], check=True)
+    out = subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.split("\n")
+    got = {tuple(l.split()[:2]): int(l.split()[2]) for l in out if l}
+    for cname, cls in _STRUCTS.items():
+        assert got[(cname, "size")] == C.sizeof(cls), cname
+        for f, _ in cls._fields_:
+            assert got[(cname, f)] == getattr(cls, f).offset, (cname, f)
 
 
 def test_index_builder_matches_oracle_tiny():

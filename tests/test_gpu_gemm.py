@@ -54,6 +54,36 @@ def test_gemm_permutation_exact(dev):
     assert torch.equal(ops.gemm(P.to(dev), X.to(dev)).cpu(), X[perm])
 
 
+@pytest.mark.parametrize("M,N,K,tile,cus", [(1024, 2560, 1024, 256, 0), (768, 1024, 2048, 128, 0),
+                                             (1024, 2560, 512, 256, 96), (2048, 2048, 1024, 256, 200)])
+def test_gemm_split_tail(dev, M, N, K, tile, cus):
+    """Tail round split along K through the workspace: matches the oracle and
+    the unsplit GEMM, twice in a row on one workspace (flags left zeroed)."""
+    _say(f"gemm split M={M} N={N} K={K} tile={tile} cus={cus}")
+    A = wl.randn_bf16((M, K), 20, K ** -0.5).to(dev)
+    B = wl.randn_bf16((K, N), 21, K ** -0.5).to(dev)
+    ws = torch.zeros(int(ops.capi.lib().mk_query_workspace_bytes(0, M, N, K)), dtype=torch.uint8, device=dev)
+    plain = ops.gemm(A, B, tile_m=tile, num_cus=cus, split_ws=False)
+    ref = gemm_ref(A.cpu(), B.cpu())
+    for _ in range(2):
+        C = ops.gemm(A, B, tile_m=tile, num_cus=cus, split_ws=ws)
+        torch.cuda.synchronize()
+        assert rel_fro(C.float(), ref) < TOL
+        assert torch.allclose(C.cpu().float(), ref, rtol=2 ** -7, atol=1e-5)
+        # fp32 partial sums differ from the unsplit order by fp32 rounding only
+        assert torch.allclose(C.float(), plain.float(), rtol=2 ** -7, atol=1e-5)
+    assert int(ws[:4096].view(torch.int32).abs().sum()) == 0, "split flags not left zeroed"
+
+
+def test_gemm_split_identity_exact(dev):
+    """With a 4-way K split, I @ X is still exact (partials are exact sums)."""
+    n = 1024
+    I = torch.eye(n, dtype=torch.bfloat16, device=dev)
+    X = wl.randn_bf16((n, n), 22).to(dev)
+    assert torch.equal(ops.gemm(I, X, tile_m=256).cpu(), X.cpu())
+    assert torch.equal(ops.gemm(X, I, tile_m=128).cpu(), X.cpu())
+
+
 def test_gemm_bad_shape_raises(dev):
     A = torch.zeros((100, 64), dtype=torch.bfloat16, device=dev)
     B = torch.zeros((64, 256), dtype=torch.bfloat16, device=dev)
@@ -126,20 +156,28 @@ def test_ag_gemm_epochs_and_orders(dev):
 def test_ag_gemm_cooperative_staging_capped_grid(dev, num_cus, K):
     """Cooperative staging with a capped grid (every workgroup copies many
     pieces and computes several rounds of tiles): staged bytes and flags
-    exact, result bit-equal to the ungated GEMM, over several epochs."""
+    exact, result bit-equal to the ungated GEMM, over several epochs.  With
+    3 workgroups the 16 tiles leave one tail tile, split 3 ways along K while
+    whole tiles follow the arrival order (a regression case: a whole tile at
+    a permuted position past the split boundary once waited on the split
+    flags).  Waits are bounded so a protocol error reports instead of
+    hanging."""
     _say(f"ag_gemm cooperative num_cus={num_cus} K={K}")
     cfg, A, B, order = _ag_case(dev, K=K)
     Ad, Bd = A.to(dev), B.to(dev)
     flags = torch.zeros(cfg.M // 128, dtype=torch.int32, device=dev)
     counters = torch.zeros_like(flags)
+    err = torch.zeros(1, dtype=torch.int32, device=dev)
     C_ref = torch.empty((cfg.M, cfg.N), dtype=torch.bfloat16, device=dev)
-    ops.ag_gemm(None, Ad, Bd, C_ref, None, None, epoch=1, gated=False, num_producers=0)
+    ops.ag_gemm(None, Ad, Bd, C_ref, None, None, epoch=1, gated=False, num_producers=0, num_cus=num_cus,
+                spin_limit=4_000_000, error_word=err)
     for epoch in (1, 2, 4):
         A_full = torch.zeros_like(Ad)
         C = torch.empty_like(C_ref)
         ops.ag_gemm(Ad, A_full, Bd, C, flags, order.to(dev), epoch=epoch, num_producers=-1, num_cus=num_cus,
-                    stage_counters=counters)
+                    stage_counters=counters, spin_limit=4_000_000, error_word=err)
         torch.cuda.synchronize()
+        assert int(err.item()) == 0, "a bounded wait timed out"
         assert torch.equal(A_full.cpu(), A)
         assert (flags.cpu() == epoch).all()
         assert torch.equal(C.cpu(), C_ref.cpu())
