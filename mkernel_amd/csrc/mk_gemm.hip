@@ -124,19 +124,22 @@ __device__ void producer_role(const GemmKParams& p, int pid) {
 }
 
 // Cooperative staging: every compute workgroup copies its share of the
-// staging pieces (kPieces per 128-row block, taken in stage order so the
-// earliest-needed blocks complete first) before it starts computing.  Each
-// finished piece bumps its block's counter; the workgroup whose increment
-// completes the block publishes the block's flag.  Counters are never reset:
-// completion is detected modulo kPieces.
+// staging pieces (kPieces per 128-row block; global piece q is piece
+// q % kPieces of the block at stage position q / kPieces, and workgroup c
+// owns pieces c, c + n_cons, ...).  Each finished piece bumps its block's
+// counter; the workgroup whose increment completes the block publishes the
+// block's flag.  Counters are never reset: completion is detected modulo
+// kPieces.  A workgroup stages in increasing q and may stop at any limit and
+// resume later (q and batch are its cursor), which lets the copy run between
+// tile rounds instead of all before the first one.
 template <int NT>
-__device__ void coop_stage(const GemmKParams& p, int cid) {
+__device__ void coop_stage(const GemmKParams& p, int cid, int& q, int& batch, int limit) {
   const int64_t block_elems = (int64_t)kFlagRows * p.st_cols;
   const int64_t piece_vec = block_elems / 8 / kPieces;  // 16-byte units per piece
-  const int total = p.st_nblocks * kPieces;
+  limit = min(limit, p.st_nblocks * kPieces);
   constexpr int U = 16;
-  auto copy_piece = [&](int q) {
-    const int pos = q / kPieces, piece = q % kPieces;
+  auto copy_piece = [&](int qq) {
+    const int pos = qq / kPieces, piece = qq % kPieces;
     const int b = p.st_order ? p.st_order[pos] : pos;
     const u32x4_t* src = reinterpret_cast<const u32x4_t*>(p.st_src + (int64_t)b * block_elems) + piece * piece_vec;
     u32x4_t* dst = reinterpret_cast<u32x4_t*>(p.st_dst + (int64_t)b * block_elems) + piece * piece_vec;
@@ -162,11 +165,10 @@ __device__ void coop_stage(const GemmKParams& p, int cid) {
   // barrier, one agent-scope release (an L2 write-back), then count the
   // batch's pieces.  Fewer releases cost fewer serialised write-backs; the
   // first batch is a single piece so the earliest blocks complete early.
-  int q = cid, batch = 1;
-  while (q < total) {
+  while (q < limit) {
     int bs[8];
     int n = 0;
-    for (; n < batch && q < total; ++n, q += p.n_cons) bs[n] = copy_piece(q);
+    for (; n < batch && q < limit; ++n, q += p.n_cons) bs[n] = copy_piece(q);
     __syncthreads();
     if (threadIdx.x == 0) {
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
@@ -252,28 +254,50 @@ __device__ __forceinline__ void store_tile(const GemmKParams& p, f32x16 (&acc)[C
             wait_flag(p.rs_flags + (f / per) * rbs + lr0 / kFlagRows + f % per, p.epoch, p.spin_limit, p.err);
         __syncthreads();
       }
+      // Fold the peers' bf16 partials into the fp32 accumulators, peer by
+      // peer in rank order (deterministic).  All of one peer's loads are
+      // issued before any is consumed (one memory latency per peer, not per
+      // element); buffer loads keep the per-element offsets as immediates.
       const int64_t peer_stride = (int64_t)p.rs_own_rows * p.ldc;
+      uint32_t voff[C::FM];
+#pragma unroll
+      for (int i = 0; i < C::FM; ++i)
+        voff[i] = (uint32_t)(((wm * C::WTM + i * 32 + ml) * p.ldc + tn * kBN + wn * C::WTN + 4 * kg) * 2);
+      for (int q = 0; q < p.rs_npeers; ++q) {
+        const __amdgpu_buffer_rsrc_t r =
+            make_rsrc(p.rs_recv + q * peer_stride + (int64_t)lr0 * p.ldc, (uint32_t)(C::BM * p.ldc * 2));
+        uint2 v[C::FM][C::FN][4];
+#pragma unroll
+        for (int i = 0; i < C::FM; ++i)
+#pragma unroll
+          for (int j = 0; j < C::FN; ++j)
+#pragma unroll
+            for (int a = 0; a < 4; ++a)
+              v[i][j][a] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(r, voff[i] + (j * 32 + 8 * a) * 2, 0, 0));
+#pragma unroll
+        for (int i = 0; i < C::FM; ++i)
+#pragma unroll
+          for (int j = 0; j < C::FN; ++j)
+#pragma unroll
+            for (int a = 0; a < 4; ++a) {
+              acc[i][j][4 * a + 0] += bf16_lo(v[i][j][a].x);
+              acc[i][j][4 * a + 1] += bf16_hi(v[i][j][a].x);
+              acc[i][j][4 * a + 2] += bf16_lo(v[i][j][a].y);
+              acc[i][j][4 * a + 3] += bf16_hi(v[i][j][a].y);
+            }
+      }
 #pragma unroll
       for (int i = 0; i < C::FM; ++i) {
         const int lr = lr0 + wm * C::WTM + i * 32 + ml;
-        const int64_t off = (int64_t)lr * p.ldc + tn * kBN + wn * C::WTN + 4 * kg;
+        uint16_t* orow = p.rs_out + (int64_t)lr * p.ldc + tn * kBN + wn * C::WTN + 4 * kg;
 #pragma unroll
         for (int j = 0; j < C::FN; ++j)
 #pragma unroll
           for (int a = 0; a < 4; ++a) {
-            float s0 = acc[i][j][4 * a + 0], s1 = acc[i][j][4 * a + 1];
-            float s2 = acc[i][j][4 * a + 2], s3 = acc[i][j][4 * a + 3];
-            for (int q = 0; q < p.rs_npeers; ++q) {
-              const uint2 w = *reinterpret_cast<const uint2*>(p.rs_recv + q * peer_stride + off + j * 32 + 8 * a);
-              s0 += bf16_lo(w.x);
-              s1 += bf16_hi(w.x);
-              s2 += bf16_lo(w.y);
-              s3 += bf16_hi(w.y);
-            }
             uint2 w;
-            w.x = pack_bf16x2(s0, s1);
-            w.y = pack_bf16x2(s2, s3);
-            *reinterpret_cast<uint2*>(p.rs_out + off + j * 32 + 8 * a) = w;
+            w.x = pack_bf16x2(acc[i][j][4 * a + 0], acc[i][j][4 * a + 1]);
+            w.y = pack_bf16x2(acc[i][j][4 * a + 2], acc[i][j][4 * a + 3]);
+            *reinterpret_cast<uint2*>(orow + j * 32 + 8 * a) = w;
           }
       }
     }
@@ -356,6 +380,13 @@ __device__ __forceinline__ bf16x4_t lds_tr4(const char* p) {
       (__attribute__((address_space(3))) bf16x4_t*)((__attribute__((address_space(3))) char*)(p)));
 }
 
+// Cursor of a workgroup's cooperative staging between tile rounds.
+struct StagePlan {
+  const int* round_need;  // per round: last stage position it waits for (null: staged up front)
+  int n_rounds;
+  int q, batch;           // coop_stage cursor
+};
+
 // Partial-sum exchange for K-split tail tiles.  A tile's NT threads hold
 // FM*FN*16 fp32 accumulators each; they go to the workspace as 16-byte
 // units in register order, unit ((i*FN + j)*4 + a)*NT + tid, so writes and
@@ -409,7 +440,7 @@ __device__ __forceinline__ void add_partial(const float* src, f32x16 (&acc)[C::F
 // ---------------------------------------------------------------------------
 template <class C, int EPI>
 __device__ void compute_role(const GemmKParams& p, int cons_id, char* smem, const int* row_perm,
-                             const uint16_t* full_list) {
+                             const uint16_t* full_list, StagePlan& sp) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
@@ -643,7 +674,15 @@ __device__ void compute_role(const GemmKParams& p, int cons_id, char* smem, cons
   // split set; the split set is the last tiles of the unpermuted order, so
   // which tiles are split, and hence every output bit, does not depend on
   // the arrival order.
+  const int st_total = p.st_nblocks * kPieces;
   for (int w = 0; w < n_full_mine; ++w) {
+    if (sp.round_need) {
+      // this tile is in round w: stage what round w waits for, and at least
+      // an even share of the rest
+      const int need = (sp.round_need[w] + 1) * kPieces;
+      const int even = (int)((int64_t)st_total * (w + 1) / sp.n_rounds);
+      coop_stage<C::NT>(p, cons_id, sp.q, sp.batch, max(need, even));
+    }
     int t = cons_id + w * p.n_cons;
     if (full_list) t = full_list[t];
     f32x16 acc[C::FM][C::FN];
@@ -651,6 +690,7 @@ __device__ void compute_role(const GemmKParams& p, int cons_id, char* smem, cons
     tile_body(t, row_perm != nullptr, 0, nk_all, acc, m0, tn);
     store_tile<C, EPI>(p, acc, m0, tn, tid);
   }
+  if (sp.round_need) coop_stage<C::NT>(p, cons_id, sp.q, sp.batch, st_total);
   if (cons_id >= n_tail_units) return;
   // The K-split unit: tail tile full + tail_idx (unpermuted), K part `part`.
   const int tail_idx = cons_id / p.sk_split;
@@ -689,7 +729,7 @@ __device__ void compute_role(const GemmKParams& p, int cons_id, char* smem, cons
 // compute follows arrival; for the reduce epilogue, non-owned rows first and
 // owned rows last.
 template <int BM, int NT>
-__device__ void build_row_perm(const GemmKParams& p, int* row_perm, int* scratch) {
+__device__ void build_row_perm(const GemmKParams& p, int* row_perm, int* row_key, int* scratch) {
   const int tid = threadIdx.x;
   const int tm = p.tiles_m;
   if (p.perm_mode == kPermArrival) {
@@ -713,6 +753,7 @@ __device__ void build_row_perm(const GemmKParams& p, int* row_perm, int* scratch
         rank += (kj < key) || (kj == key && j < i);
       }
       row_perm[rank] = i;
+      row_key[rank] = key;
     }
   } else {  // kPermOwnedLast
     const int own0 = p.rs_own_row0 / BM, nown = p.rs_own_rows / BM;
@@ -721,7 +762,29 @@ __device__ void build_row_perm(const GemmKParams& p, int* row_perm, int* scratch
       if (i < tm - nown) r = i < own0 ? i : i + nown;
       else r = own0 + (i - (tm - nown));
       row_perm[i] = r;
+      // the owned rows need every staged peer block, the others none
+      row_key[i] = (r >= own0 && r < own0 + nown) ? p.st_nblocks - 1 : -1;
     }
+  }
+  __syncthreads();
+}
+
+// Staging need of each whole-tile round: round_need[r] = the last stage
+// position any tile of round r (whole tiles i = r*n_cons .. (r+1)*n_cons-1
+// of the schedule) waits for.  Staging every piece up to that position
+// before round r, in every workgroup, lets round r complete without waiting
+// on a workgroup that is still in an earlier round.
+template <int NT>
+__device__ void build_round_need(const GemmKParams& p, int full, int n_rounds, const uint16_t* full_list,
+                                 const int* row_key, int* round_need) {
+  const int tid = threadIdx.x;
+  for (int r = tid; r < n_rounds; r += NT) round_need[r] = -1;
+  __syncthreads();
+  for (int i = tid; i < full; i += NT) {
+    const int t = full_list ? full_list[i] : i;
+    int tm, tn;
+    decode_grouped(t, p.tiles_m, p.tiles_n, p.group_m, tm, tn);
+    atomicMax(&round_need[i / p.n_cons], row_key[tm]);
   }
   __syncthreads();
 }
@@ -771,19 +834,20 @@ __global__ __launch_bounds__(64 * WAVES, 1) void gemm_kernel(GemmKParams p) {
   extern __shared__ __attribute__((aligned(16))) char smem[];
   __shared__ int row_perm[kMaxTilesM];
   __shared__ uint16_t full_list[kMaxSplitListTiles];
+  __shared__ int row_key[kMaxTilesM];
+  __shared__ int round_need[kMaxRounds];
   if ((int)blockIdx.x < p.n_prod) {
     producer_role<C::NT>(p, blockIdx.x);
     return;
   }
   int cons = blockIdx.x - p.n_prod;
-  if (p.st_coop) coop_stage<C::NT>(p, cons);
   // XCD-aware renumbering: workgroups are dealt round-robin to the 8 XCDs,
   // so give each XCD a contiguous run of consumer ids (hence of tiles, which
   // the grouped order keeps close in A rows / B columns) for L2 reuse.
   if (p.xcd_remap) cons = (cons % 8) * (p.n_cons / 8) + cons / 8;
   const int* perm = nullptr;
   if (p.perm_mode != kPermNone) {
-    build_row_perm<BM, C::NT>(p, row_perm, reinterpret_cast<int*>(smem));
+    build_row_perm<BM, C::NT>(p, row_perm, row_key, reinterpret_cast<int*>(smem));
     perm = row_perm;
   }
   const uint16_t* flist = nullptr;
@@ -791,7 +855,27 @@ __global__ __launch_bounds__(64 * WAVES, 1) void gemm_kernel(GemmKParams p) {
     build_full_list<C::NT>(p, row_perm, full_list, reinterpret_cast<int*>(smem));
     flist = full_list;
   }
-  compute_role<C, EPI>(p, cons, smem, perm, flist);
+  // Cooperative staging runs between tile rounds when the schedule's
+  // staging needs are known (a permuted order with at most kMaxRounds
+  // rounds); otherwise all of it runs before the first tile.
+  StagePlan sp;
+  sp.q = cons;
+  sp.batch = 1;
+  sp.n_rounds = 0;
+  sp.round_need = nullptr;
+  if (p.st_coop) {
+    const int ntiles = p.tiles_m * p.tiles_n;
+    const int full = (p.sk_split > 1) ? p.sk_full : ntiles;
+    const int n_rounds = (full + p.n_cons - 1) / p.n_cons;
+    if (perm && n_rounds <= kMaxRounds) {
+      build_round_need<C::NT>(p, full, n_rounds, flist, row_key, round_need);
+      sp.n_rounds = n_rounds;
+      sp.round_need = round_need;
+    } else {
+      coop_stage<C::NT>(p, cons, sp.q, sp.batch, p.st_nblocks * kPieces);
+    }
+  }
+  compute_role<C, EPI>(p, cons, smem, perm, flist, sp);
 }
 
 // ---------------------------------------------------------------------------

@@ -10,6 +10,7 @@ enum Epilogue : int { kEpiStore = 0, kEpiSwiGLU = 1, kEpiReduce = 2 };
 enum PermMode : int { kPermNone = 0, kPermArrival = 1, kPermOwnedLast = 2 };
 constexpr int kMaxTilesM = 512;
 constexpr int kMaxSplitListTiles = 4096;  // K-split with a permuted tile order: at most this many tiles
+constexpr int kMaxRounds = 64;   // cooperative staging between rounds: at most this many rounds
 constexpr int kPieces = 16;  // cooperative staging: pieces per 128-row block
 
 struct GemmKParams {
