@@ -576,7 +576,7 @@ __device__ void compute_role(const GemmKParams& p, int cons_id, char* smem, cons
     auto mfma = [&](int kk) {
 #pragma unroll
       for (int i = 0; i < C::FM; ++i)
-        if (i < fm_active) {
+        if (C::BM != 128 || i < fm_active) {  // the skip is for 128-row expert tiles only
 #pragma unroll
           for (int j = 0; j < C::FN; ++j)
             acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[kk][j], af[kk][i], acc[i][j], 0, 0, 0);
@@ -603,6 +603,11 @@ __device__ void compute_role(const GemmKParams& p, int cons_id, char* smem, cons
         read_frags(j % C::S, 1);
       };
       auto wait_j = [&](int j) { wait_stage<C::S + 1, C::LOADS>(min(C::S - 2, nk - 1 - j)); };
+      // wait for stage j+1 (steady state: S-2 younger stages in flight)
+      auto wait_next = [&](int j) {
+        if (j + C::S - 1 < nk) wait_vm<(C::S - 2) * C::LOADS>();
+        else if (j + 1 < nk) wait_j(j + 1);
+      };
       auto bar = [] {
         __builtin_amdgcn_sched_barrier(0);
         __syncthreads();
@@ -621,7 +626,7 @@ __device__ void compute_role(const GemmKParams& p, int cons_id, char* smem, cons
           bar();
           mfma(0);
           mfma(1);
-          if (j + 1 < nk) wait_j(j + 1);
+          wait_next(j);
           bar();
           if (j + 1 < nk) mem_step(j + 1);
         }
@@ -629,7 +634,7 @@ __device__ void compute_role(const GemmKParams& p, int cons_id, char* smem, cons
         for (int j = 0; j < nk; ++j) {
           bar();
           mem_step(j);
-          if (j + 1 < nk) wait_j(j + 1);
+          wait_next(j);
           bar();
           mfma(0);
           mfma(1);
