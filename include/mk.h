@@ -200,6 +200,8 @@ typedef struct mk_moe_grouped_gemm_args {
   int32_t num_experts;
   int32_t mode;
   int32_t num_cus;
+  void* split_ws;              /* optional K-split workspace, as in mk_gemm_args */
+  int64_t split_ws_bytes;
 } mk_moe_grouped_gemm_args;
 int mk_moe_grouped_gemm(const mk_moe_grouped_gemm_args* args, void* stream);
 
@@ -254,6 +256,8 @@ typedef struct mk_moe_ffn_args {
   int32_t tokens_per_src, devs_per_node;
   int32_t out_dtype;
   int32_t num_cus;
+  void* split_ws;              /* optional K-split workspace, as in mk_gemm_args */
+  int64_t split_ws_bytes;
 } mk_moe_ffn_args;
 int mk_moe_ffn_combine(const mk_moe_ffn_args* args, void* stream);
 

@@ -398,7 +398,8 @@ int mk_moe_permute(const mk_moe_permute_args* a, void* stream) {
 
 static int grouped_gemm_impl(const void* A, const void* W, void* out, const int32_t* rb_expert,
                              const int32_t* expert_rows, const int32_t* rb_rows, int64_t R_pad, int64_t K,
-                             int64_t Nw, int32_t E, int32_t mode, int32_t num_cus, hipStream_t stream) {
+                             int64_t Nw, int32_t E, int32_t mode, int32_t num_cus, void* split_ws,
+                             int64_t split_ws_bytes, hipStream_t stream) {
   if (!A || !W || !out || (!rb_expert && !expert_rows)) return fail(MK_EINVAL, "mk_moe_grouped_gemm: null argument");
   if (mode != 0 && mode != 1) return fail(MK_EINVAL, "mk_moe_grouped_gemm: mode must be 0 or 1");
   if (E <= 0) return fail(MK_EINVAL, "mk_moe_grouped_gemm: num_experts must be positive");
@@ -423,6 +424,8 @@ static int grouped_gemm_impl(const void* A, const void* W, void* out, const int3
   p.swiglu_I = (int)(Nw / 2);
   const int total = num_cus > 0 ? num_cus : d.cus;
   set_grid(p, total, 0, p.tiles_m * p.tiles_n);
+  if (int rc = check_ws(split_ws, split_ws_bytes, "mk_moe_grouped_gemm")) return rc;
+  plan_split(p, 128, split_ws, split_ws_bytes);
   hipError_t e = mk::launch_gemm(p, 128, mode == 1 ? mk::kEpiSwiGLU : mk::kEpiStore, stream);
   return e == hipSuccess ? MK_OK : hip_fail(e, "mk_moe_grouped_gemm launch");
 }
@@ -430,7 +433,7 @@ static int grouped_gemm_impl(const void* A, const void* W, void* out, const int3
 int mk_moe_grouped_gemm(const mk_moe_grouped_gemm_args* a, void* stream) {
   if (!a) return fail(MK_EINVAL, "mk_moe_grouped_gemm: null argument");
   return grouped_gemm_impl(a->A, a->W, a->out, a->rb_expert, a->padded_tokens_per_expert, a->rb_rows, a->R_pad, a->K, a->Nw, a->num_experts, a->mode,
-                           a->num_cus, static_cast<hipStream_t>(stream));
+                           a->num_cus, a->split_ws, a->split_ws_bytes, static_cast<hipStream_t>(stream));
 }
 
 int mk_moe_combine(const mk_moe_combine_args* a, void* stream) {
@@ -475,11 +478,11 @@ int mk_moe_ffn_combine(const mk_moe_ffn_args* a, void* stream) {
   if (int rc = mk_moe_permute(&pa, stream)) return rc;
   if (int rc = grouped_gemm_impl(a->post_tokens, a->w1, a->act, a->rb_expert, a->padded_tokens_per_expert,
                                  a->rb_rows, a->R_pad,
-                                 a->H, 2 * a->I, a->num_experts, 1, a->num_cus, s))
+                                 a->H, 2 * a->I, a->num_experts, 1, a->num_cus, a->split_ws, a->split_ws_bytes, s))
     return rc;
   if (int rc = grouped_gemm_impl(a->act, a->w2, a->y_expert, a->rb_expert, a->padded_tokens_per_expert,
                                  a->rb_rows, a->R_pad,
-                                 a->I, a->H, a->num_experts, 0, a->num_cus, s))
+                                 a->I, a->H, a->num_experts, 0, a->num_cus, a->split_ws, a->split_ws_bytes, s))
     return rc;
   mk_moe_combine_args ca{a->y_expert, a->row_weight, a->owner_offset, a->slot_to_row, a->y_out,
                          a->num_tokens, a->H, a->out_dtype};

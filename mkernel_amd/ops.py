@@ -147,13 +147,13 @@ def moe_permute(tokens, pull, post, tokens_per_src: int | None = None, devs_per_
 
 
 def moe_grouped_gemm(A, W, out, rb_expert=None, padded_tokens_per_expert=None, mode: int = 0, num_cus: int = 0,
-                     rb_rows=None):
+                     rb_rows=None, split_ws=None):
     """mode 0: out = A @ W[e]; mode 1: out = silu(h[:, :I]) * h[:, I:], h = A @ W[e]."""
     _bf16(A, "A"); _bf16(W, "W"); _bf16(out, "out")
     R_pad, K = A.shape
     E, _, Nw = W.shape
     args = MoeGroupedGemmArgs(_ptr(A), _ptr(W), _ptr(out), _ptr(rb_expert), _ptr(padded_tokens_per_expert),
-                              _ptr(rb_rows), R_pad, K, Nw, E, mode, num_cus)
+                              _ptr(rb_rows), R_pad, K, Nw, E, mode, num_cus, *_ws(split_ws, A.device))
     capi.call("mk_moe_grouped_gemm", args, _stream())
     return out
 
@@ -184,7 +184,7 @@ def moe_combine(y_expert, row_weight, owner_offset, slot_to_row, y_out):
 
 def moe_ffn_combine(tokens, pull, row_weight, owner_offset, slot_to_row, w1, w2, post, act, y_expert, y_out,
                     rb_expert=None, padded_tokens_per_expert=None, tokens_per_src: int | None = None,
-                    devs_per_node: int = 1, num_cus: int = 0, rb_rows=None):
+                    devs_per_node: int = 1, num_cus: int = 0, rb_rows=None, split_ws=None):
     """permute -> grouped GEMM1 + SwiGLU -> grouped GEMM2 -> combine."""
     T, H = y_out.shape
     E, _, I2 = w1.shape
@@ -194,6 +194,7 @@ def moe_ffn_combine(tokens, pull, row_weight, owner_offset, slot_to_row, w1, w2,
     args = MoeFfnArgs(_ptr(tokens), _ptr(pull), _ptr(rb_expert), _ptr(padded_tokens_per_expert), _ptr(rb_rows),
                       _ptr(row_weight),
                       _ptr(owner_offset), _ptr(slot_to_row), _ptr(w1), _ptr(w2), _ptr(post), _ptr(act), _ptr(y_expert),
-                      _ptr(y_out), T, tokens.shape[0], R_pad, H, I2 // 2, E, tps, devs_per_node, od, num_cus)
+                      _ptr(y_out), T, tokens.shape[0], R_pad, H, I2 // 2, E, tps, devs_per_node, od, num_cus,
+                      *_ws(split_ws, tokens.device))
     capi.call("mk_moe_ffn_combine", args, _stream())
     return y_out

@@ -34,15 +34,18 @@ def test_permute_bit_exact(dev):
     assert torch.equal(post.cpu(), om.permute_ref(tokens, idx["pull_indices"]))
 
 
+@pytest.mark.parametrize("split", [None, False])
 @pytest.mark.parametrize("use_rb,skip_pad", [(True, False), (False, False), (True, True)])
-def test_grouped_gemm1(dev, use_rb, skip_pad):
-    _say(f"moe grouped gemm1 use_rb={use_rb} skip_pad={skip_pad}")
+def test_grouped_gemm1(dev, use_rb, skip_pad, split):
+    """split None: the tail round is K-split through the default workspace;
+    False: no K-split."""
+    _say(f"moe grouped gemm1 use_rb={use_rb} skip_pad={skip_pad} split={split}")
     tokens, ids, gates, w1, w2, idx, d = _setup(dev)
     post = om.permute_ref(tokens, idx["pull_indices"])
     out = torch.full((idx["R_pad"], 2 * SMALL.I), 3.0, dtype=torch.bfloat16, device=dev)
     ops.moe_grouped_gemm(post.to(dev), w1.to(dev), out, rb_expert=d["rb_expert"] if use_rb else None,
                          padded_tokens_per_expert=None if use_rb else d["padded_tokens_per_expert"], mode=0,
-                         rb_rows=d["rb_rows"] if skip_pad else None)
+                         rb_rows=d["rb_rows"] if skip_pad else None, split_ws=split)
     torch.cuda.synchronize()
     ref = om.grouped_gemm_ref(post, w1, idx["padded_tokens_per_expert"])
     assert rel_fro(out.float(), ref) < TOL
@@ -50,12 +53,13 @@ def test_grouped_gemm1(dev, use_rb, skip_pad):
     assert (out.cpu()[torch.from_numpy(pad)] == 0).all()  # zero rows stay zero
 
 
-def test_gemm1_swiglu(dev):
-    _say("moe gemm1+swiglu")
+@pytest.mark.parametrize("split", [None, False])
+def test_gemm1_swiglu(dev, split):
+    _say(f"moe gemm1+swiglu split={split}")
     tokens, ids, gates, w1, w2, idx, d = _setup(dev)
     post = om.permute_ref(tokens, idx["pull_indices"])
     act = torch.empty((idx["R_pad"], SMALL.I), dtype=torch.bfloat16, device=dev)
-    ops.moe_grouped_gemm(post.to(dev), w1.to(dev), act, rb_expert=d["rb_expert"], mode=1)
+    ops.moe_grouped_gemm(post.to(dev), w1.to(dev), act, rb_expert=d["rb_expert"], mode=1, split_ws=split)
     torch.cuda.synchronize()
     ref_act, _ = om.ffn_ref(post, w1, w2, idx["padded_tokens_per_expert"], SMALL.I)
     assert rel_fro(act.float(), ref_act) < TOL
