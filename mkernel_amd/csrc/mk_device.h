@@ -90,4 +90,38 @@ __device__ __forceinline__ void publish_flag(uint32_t* flag, uint32_t epoch) {
   __hip_atomic_store(flag, epoch, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// s_waitcnt vmcnt(0), other counters untouched (gfx9 encoding).
+__device__ __forceinline__ void wait_vmem_all() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
+// Write-through staging copy of `nvec` 16-byte units, `NT` threads, U loads
+// in flight per thread.  Loads are nontemporal; stores are buffer stores
+// with SC1 and NT set: SC1 makes each store coherent at agent scope (the
+// form the AMDGPU memory model gives a relaxed agent-scope atomic store:
+// written through the XCD's L2), NT keeps the bytes out of the caches.
+// Publication protocol built on it: every wave waits vmcnt(0) for its own
+// stores (after which they are performed at agent scope), a workgroup
+// barrier, then one thread's relaxed agent-scope atomics publish.  This is
+// the release sequence of the memory model minus its L2 write-back
+// (buffer_wbl2), which is only needed for data written without SC1 — and
+// that write-back flushes every dirty line of the XCD's L2, which cost the
+// staging ~15 % of the launch when it ran once per published batch.
+template <int NT, int U>
+__device__ __forceinline__ void copy_wt(const void* src, void* dst, int64_t nvec) {
+  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+  const u32x4* s = static_cast<const u32x4*>(src);
+  const __amdgpu_buffer_rsrc_t r = make_rsrc(dst, (uint32_t)(nvec * 16));
+  constexpr int kCpolScNt = 0x12;  // gfx940+ cache policy: SC1 | NT
+  int64_t base = threadIdx.x;
+  for (; base + (int64_t)(U - 1) * NT < nvec; base += (int64_t)U * NT) {
+    u32x4 v[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) v[u] = __builtin_nontemporal_load(s + base + u * NT);
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      __builtin_amdgcn_raw_buffer_store_b128(v[u], r, (int)((base + u * NT) * 16), 0, kCpolScNt);
+  }
+  for (; base < nvec; base += NT)
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_nontemporal_load(s + base), r, (int)(base * 16), 0, kCpolScNt);
+}
+
 }  // namespace mk

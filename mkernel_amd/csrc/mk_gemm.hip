@@ -98,28 +98,13 @@ __device__ __forceinline__ int b_col(const GemmKParams& p, int tn, int q) {
 template <int NT>
 __device__ void producer_role(const GemmKParams& p, int pid) {
   const int64_t block_elems = (int64_t)kFlagRows * p.st_cols;
-  const int64_t block_vec = block_elems / 8;  // 16-byte units
-  constexpr int U = 16;                       // 16-byte loads in flight per thread
   for (int i = pid; i < p.st_nblocks; i += p.n_prod) {
     const int b = p.st_order ? p.st_order[i] : i;
-    // Streaming copy: nontemporal loads and stores keep the staged bytes
-    // out of the caches the compute role is using.
-    const u32x4_t* src = reinterpret_cast<const u32x4_t*>(p.st_src + (int64_t)b * block_elems);
-    u32x4_t* dst = reinterpret_cast<u32x4_t*>(p.st_dst + (int64_t)b * block_elems);
-    int64_t base = threadIdx.x;
-    for (; base + (int64_t)(U - 1) * NT < block_vec; base += (int64_t)U * NT) {
-      u32x4_t v[U];
-#pragma unroll
-      for (int u = 0; u < U; ++u) v[u] = __builtin_nontemporal_load(src + base + u * NT);
-#pragma unroll
-      for (int u = 0; u < U; ++u) __builtin_nontemporal_store(v[u], dst + base + u * NT);
-    }
-    for (; base < block_vec; base += NT) __builtin_nontemporal_store(__builtin_nontemporal_load(src + base), dst + base);
-    // The barrier waits for every wave's stores; thread 0's agent-scope
-    // release then makes the whole block visible (one L2 write-back per
-    // block, not one per wave).
+    copy_wt<NT, 16>(p.st_src + (int64_t)b * block_elems, p.st_dst + (int64_t)b * block_elems, block_elems / 8);
+    // every wave's write-through stores performed, then one publication
+    wait_vmem_all();
     __syncthreads();
-    if (threadIdx.x == 0) publish_flag(p.st_flags + b, p.epoch);
+    if (threadIdx.x == 0) __hip_atomic_store(p.st_flags + b, p.epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }
 
@@ -137,43 +122,33 @@ __device__ void coop_stage(const GemmKParams& p, int cid, int& q, int& batch, in
   const int64_t block_elems = (int64_t)kFlagRows * p.st_cols;
   const int64_t piece_vec = block_elems / 8 / kPieces;  // 16-byte units per piece
   limit = min(limit, p.st_nblocks * kPieces);
-  constexpr int U = 16;
   auto copy_piece = [&](int qq) {
     const int pos = qq / kPieces, piece = qq % kPieces;
     const int b = p.st_order ? p.st_order[pos] : pos;
-    const u32x4_t* src = reinterpret_cast<const u32x4_t*>(p.st_src + (int64_t)b * block_elems) + piece * piece_vec;
-    u32x4_t* dst = reinterpret_cast<u32x4_t*>(p.st_dst + (int64_t)b * block_elems) + piece * piece_vec;
-    int64_t base = threadIdx.x;
-    for (; base + (int64_t)(U - 1) * NT < piece_vec; base += (int64_t)U * NT) {
-      u32x4_t v[U];
-#pragma unroll
-      for (int u = 0; u < U; ++u) v[u] = __builtin_nontemporal_load(src + base + u * NT);
-#pragma unroll
-      for (int u = 0; u < U; ++u) __builtin_nontemporal_store(v[u], dst + base + u * NT);
-    }
-    for (; base < piece_vec; base += NT) __builtin_nontemporal_store(__builtin_nontemporal_load(src + base), dst + base);
+    const int64_t off = (int64_t)b * block_elems + (int64_t)piece * piece_vec * 8;
+    copy_wt<NT, 16>(p.st_src + off, p.st_dst + off, piece_vec);
     return b;
   };
+  // The counter increments form one chain per block; each is made after
+  // its workgroup's pieces were performed at agent scope (copy_wt), so the
+  // workgroup whose increment completes the block may publish the flag with
+  // a relaxed agent-scope store.
   auto count_piece = [&](int b) {
     const uint32_t old = __hip_atomic_fetch_add(p.st_counters + b, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (old % kPieces == kPieces - 1) {
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-      publish_flag(p.st_flags + b, p.epoch);
-    }
+    if (old % kPieces == kPieces - 1)
+      __hip_atomic_store(p.st_flags + b, p.epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   };
-  // Pieces are released in batches of p.st_batch: copy the batch, one
-  // barrier, one agent-scope release (an L2 write-back), then count the
-  // batch's pieces.  Fewer releases cost fewer serialised write-backs; the
-  // first batch is a single piece so the earliest blocks complete early.
+  // Pieces are counted in batches of p.st_batch: copy the batch, wait for
+  // the stores, one barrier, then count the batch's pieces; the first batch
+  // is a single piece so the earliest blocks complete early.
   while (q < limit) {
     int bs[8];
     int n = 0;
     for (; n < batch && q < limit; ++n, q += p.n_cons) bs[n] = copy_piece(q);
+    wait_vmem_all();
     __syncthreads();
-    if (threadIdx.x == 0) {
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    if (threadIdx.x == 0)
       for (int i = 0; i < n; ++i) count_piece(bs[i]);
-    }
     batch = p.st_batch;
   }
 }
@@ -390,7 +365,8 @@ struct StagePlan {
 // Partial-sum exchange for K-split tail tiles.  A tile's NT threads hold
 // FM*FN*16 fp32 accumulators each; they go to the workspace as 16-byte
 // units in register order, unit ((i*FN + j)*4 + a)*NT + tid, so writes and
-// reads are fully coalesced and need no layout conversion.  Buffer
+// reads are fully coalesced and need no layout conversion.  The stores are
+// write-through at agent scope (SC1, as in copy_wt).  Buffer
 // instructions keep the per-unit offsets in scalar registers (one VGPR of
 // addressing in total), which matters: the accumulators already hold most
 // of the register file.
@@ -407,7 +383,7 @@ __device__ __forceinline__ void put_partial(float* dst, f32x16 (&acc)[C::FM][C::
 #pragma unroll
         for (int b = 0; b < 4; ++b) v[b] = acc[i][j][4 * a + b];
         __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, v), r, tid * 16,
-                                               ((i * C::FN + j) * 4 + a) * C::NT * 16, 0);
+                                               ((i * C::FN + j) * 4 + a) * C::NT * 16, 0x12 /* SC1 | NT */);
       }
 }
 
@@ -709,8 +685,11 @@ __device__ void compute_role(const GemmKParams& p, int cons_id, char* smem, cons
     // K-split contributor: publish the partial for part 0 of this tile.
     const int slot = tail_idx * (p.sk_split - 1) + part - 1;
     put_partial<C>(p.sk_ws + (int64_t)slot * (C::BM * kBN), acc, tid);
+    // write-through stores performed at agent scope, then a relaxed flag
+    // (the protocol of copy_wt: no L2 write-back needed)
+    wait_vmem_all();
     __syncthreads();
-    if (tid == 0) publish_flag(p.sk_flags + slot, 1u);
+    if (tid == 0) __hip_atomic_store(p.sk_flags + slot, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     return;
   }
   {
