@@ -174,6 +174,15 @@ def bench_moe(steps, warmup, extra):
                                               d["slot_to_row"], w1, w2, post, act, ye, y, rb_expert=d["rb_expert"],
                                               rb_rows=d["rb_rows"]),
                 steps, warmup)
+    # routing index build on the GPU (tables from device top-k ids / gates)
+    ids_np, gates_np = wl.zipf_routing(cfg.tokens, cfg.experts, cfg.topk, cfg.zipf_s, 6)
+    ids_d = torch.from_numpy(np.ascontiguousarray(ids_np, np.int32)).cuda()
+    gates_d = torch.from_numpy(np.ascontiguousarray(gates_np, np.float32)).cuda()
+    ms_idx = t.run(lambda i: ops.moe_build_indices_dev(ids_d, gates_d, cfg.e0, cfg.n_local, sync=False), steps, warmup)
+    t0 = time.perf_counter()
+    for _ in range(3):
+        ops.moe_build_indices(ids_np, gates_np, cfg.e0, cfg.n_local)
+    ms_idx_host = (time.perf_counter() - t0) / 3 * 1e3
     used = idx["padded_tokens_per_expert"] > 0
     w_bytes1 = int(used.sum()) * cfg.H * 2 * cfg.I * 2
     w_bytes2 = int(used.sum()) * cfg.I * cfg.H * 2
@@ -188,6 +197,8 @@ def bench_moe(steps, warmup, extra):
                                 "hbm_bound_GBs": layer_bytes / ms5 / 1e6,
                                 "us_gemm1_swiglu": ms_g1 * 1e3, "us_gemm2": ms_g2 * 1e3, "us_combine": ms_comb * 1e3,
                                 "weight_bytes": w_bytes1 + w_bytes2}
+    extra["moe_index_build"] = {"us_gpu": ms_idx * 1e3, "us_host_cpp_1thread": ms_idx_host * 1e3,
+                                "entries": cfg.tokens * cfg.topk}
 
 
 # ------------------------------------------------------------ CPU baseline

@@ -164,6 +164,33 @@ int mk_moe_build_indices(const int32_t* topk_ids, const float* topk_gates,
                          int32_t num_tokens, int32_t topk, int32_t expert_begin,
                          int32_t n_local, int32_t row_block, const mk_moe_index* out);
 
+/* ------------------------------------------------------------------------ */
+/* The same routing index tables built on the GPU from top-k ids and gates in
+ * device memory (no host round trip), bit-identical to
+ * mk_moe_build_indices.  Row tables (pull_indices, row_expert, row_weight,
+ * row_to_slot, row_to_owner, slot_to_row) must hold `capacity_rows` rows,
+ * rb_expert / rb_rows capacity_rows / row_block entries; R and R_pad land in
+ * the device word pair `sizes` when the stream reaches them.  If R_pad >
+ * capacity_rows, sizes still reports it and rows past the capacity are not
+ * written (capacity_rows = num_tokens * topk + n_local * (row_block - 1)
+ * always suffices).  `workspace` holds mk_moe_index_workspace_bytes bytes.
+ * No counterpart in the reference, whose builders are host Python
+ * (bench/dispatch_gemm_bench.py:127-188,
+ * bench/dispatch_gemm_glu_combine_bench.py:222-293, 511-527). */
+typedef struct mk_moe_index_dev_args {
+  const int32_t* topk_ids;   /* [num_tokens, topk] device */
+  const float* topk_gates;   /* [num_tokens, topk] device */
+  int32_t num_tokens, topk, expert_begin, n_local, row_block;
+  int64_t capacity_rows;
+  void* workspace;
+  int64_t workspace_bytes;
+  int64_t* sizes;            /* device [2]: R, R_pad */
+  mk_moe_index out;          /* device pointers; NULL skips a table */
+} mk_moe_index_dev_args;
+int64_t mk_moe_index_workspace_bytes(int32_t num_tokens, int32_t topk, int32_t n_local);
+int mk_moe_build_indices_dev(const mk_moe_index_dev_args* args, void* stream);
+
+/* ------------------------------------------------------------------------ */
 /* Token permute into expert-contiguous rows:
  *   post[r] = tokens[src_row(r)]   (bit-exact copy), zero on padding rows,
  * src_row = (src_node * devs_per_node + src_dev) * tokens_per_src + src_token.

@@ -20,6 +20,8 @@ EXPORTS = (
     "mk_gemm_rs",
     "mk_moe_index_sizes",
     "mk_moe_build_indices",
+    "mk_moe_index_workspace_bytes",
+    "mk_moe_build_indices_dev",
     "mk_moe_permute",
     "mk_moe_grouped_gemm",
     "mk_moe_combine",
@@ -74,6 +76,12 @@ class MoeIndex(C.Structure):
                 ("row_to_slot", vp), ("row_to_owner", vp), ("slot_to_row", vp)]
 
 
+class MoeIndexDevArgs(C.Structure):
+    _fields_ = [("topk_ids", vp), ("topk_gates", vp), ("num_tokens", i32), ("topk", i32), ("expert_begin", i32),
+                ("n_local", i32), ("row_block", i32), ("capacity_rows", i64), ("workspace", vp),
+                ("workspace_bytes", i64), ("sizes", vp), ("out", MoeIndex)]
+
+
 class MoePermuteArgs(C.Structure):
     _fields_ = [("tokens", vp), ("pull_indices", vp), ("post_tokens", vp), ("R_pad", i64), ("H", i64),
                 ("n_src_rows", i64), ("tokens_per_src", i32), ("devs_per_node", i32)]
@@ -120,6 +128,10 @@ def lib() -> C.CDLL:
         L.mk_moe_index_sizes.restype = C.c_int
         L.mk_moe_build_indices.argtypes = [vp, vp, i32, i32, i32, i32, i32, C.POINTER(MoeIndex)]
         L.mk_moe_build_indices.restype = C.c_int
+        L.mk_moe_index_workspace_bytes.argtypes = [i32, i32, i32]
+        L.mk_moe_index_workspace_bytes.restype = i64
+        L.mk_moe_build_indices_dev.argtypes = [vp, vp]
+        L.mk_moe_build_indices_dev.restype = C.c_int
         L.mk_moe_invert_slots.argtypes = [vp, vp, i64, vp, vp]
         L.mk_moe_invert_slots.restype = C.c_int
         L.mk_moe_tile_rows.argtypes = [vp, i64, vp, vp]

@@ -120,6 +120,12 @@ int check_ws(const void* ws, int64_t bytes, const char* fn) {
 
 }  // namespace
 
+namespace mk {
+hipError_t launch_build_indices(const int32_t* ids, const float* gates, int T, int topk, int e0, int n_local,
+                                int row_block, int64_t cap, void* ws, int64_t* sizes, const mk_moe_index& out,
+                                hipStream_t stream);
+}
+
 extern "C" {
 
 const char* mk_last_error_string(void) { return g_err.c_str(); }
@@ -467,6 +473,28 @@ int mk_moe_tile_rows(const int32_t* pull_indices, int64_t R_pad, int32_t* rb_row
   if (int rc = device_info(&d)) return rc;
   hipError_t e = mk::launch_tile_rows(pull_indices, R_pad, rb_rows, static_cast<hipStream_t>(stream));
   return e == hipSuccess ? MK_OK : hip_fail(e, "mk_moe_tile_rows launch");
+}
+
+int64_t mk_moe_index_workspace_bytes(int32_t num_tokens, int32_t topk, int32_t n_local) {
+  if (num_tokens < 0 || topk <= 0 || n_local <= 0) return -1;
+  return mk::index_workspace_bytes(num_tokens, topk, n_local);
+}
+
+int mk_moe_build_indices_dev(const mk_moe_index_dev_args* a, void* stream) {
+  if (!a || !a->topk_ids || !a->topk_gates || !a->sizes) return fail(MK_EINVAL, "mk_moe_build_indices_dev: null argument");
+  if (a->num_tokens < 0 || a->topk <= 0 || a->n_local <= 0 || a->row_block <= 0 || a->expert_begin < 0)
+    return fail(MK_EINVAL, "mk_moe_build_indices_dev: bad sizes");
+  if ((int64_t)a->num_tokens * a->topk + (int64_t)a->n_local * a->row_block > (1LL << 31))
+    return fail(MK_ESHAPE, "mk_moe_build_indices_dev: too many rows for 32-bit row indices");
+  if (a->capacity_rows < 0) return fail(MK_EINVAL, "mk_moe_build_indices_dev: capacity_rows < 0");
+  if (!a->workspace || a->workspace_bytes < mk::index_workspace_bytes(a->num_tokens, a->topk, a->n_local))
+    return fail(MK_EINVAL, "mk_moe_build_indices_dev: workspace smaller than mk_moe_index_workspace_bytes");
+  DevInfo d;
+  if (int rc = device_info(&d)) return rc;
+  hipError_t e = mk::launch_build_indices(a->topk_ids, a->topk_gates, a->num_tokens, a->topk, a->expert_begin,
+                                          a->n_local, a->row_block, a->capacity_rows, a->workspace, a->sizes,
+                                          a->out, static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? MK_OK : hip_fail(e, "mk_moe_build_indices_dev launch");
 }
 
 int mk_moe_ffn_combine(const mk_moe_ffn_args* a, void* stream) {

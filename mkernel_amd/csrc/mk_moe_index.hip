@@ -1,0 +1,259 @@
+// mk_moe_index.hip — MoE routing index tables built on the GPU.
+//
+// Same tables, bit for bit, as the host builder mk_moe_build_indices (which
+// restates the reference's host-side Python builders
+// bench/dispatch_gemm_bench.py:127-188 and
+// bench/dispatch_gemm_glu_combine_bench.py:222-293, 511-527), from top-k ids
+// and gates already in device memory, with no host round trip:
+//   * rows grouped by local expert (ascending), each expert padded to a
+//     multiple of row_block; inside an expert, entries (t, k) in ascending
+//     t*topk + k order — a stable counting sort of the routed entries by
+//     expert;
+//   * pull_indices (0, 0, t) for a routed row, (-1, -1, -1) for padding;
+//   * the gather CSR: owner_offset = prefix over tokens of their routed
+//     entries, slots handed out in row order (so a token's slots follow its
+//     rows' expert order), and its inverse slot_to_row.
+//
+// Kernels (one stream, in order):
+//   count   per 256-entry chunk, per-expert counts            -> hist[e][chunk]
+//   plan    one block: per-expert totals and chunk prefixes, padded expert
+//           offsets, R and R_pad, per-expert tables           -> base[e][chunk]
+//   tokens  per token, routed entries                          -> tok[t]
+//   offsets one block: exclusive prefix of tok                 -> owner_offset
+//   scatter per chunk: stable rank within the chunk, row, slot -> routed rows
+//   pad     per row < R_pad: expert of the row, padding rows, row-block tables
+#include "../../include/mk.h"
+#include "mk_internal.h"
+
+namespace mk {
+
+constexpr int kChunk = 256;  // routed entries per count / scatter block
+
+struct IndexKParams {
+  const int32_t* ids;
+  const float* gates;
+  int T, topk, e0, n_local, row_block;
+  int64_t cap;       // rows the row tables hold
+  int nchunks;
+  int* hist;         // [n_local][nchunks] counts, then row bases
+  int* exp_off;      // [n_local + 1] padded row offset of each expert
+  int* exp_cnt;      // [n_local] routed rows of each expert
+  int* tok;          // [T] routed entries per token
+  int64_t* sizes;    // [2] R, R_pad
+  mk_moe_index out;
+};
+
+__device__ __forceinline__ int local_expert(const IndexKParams& p, int64_t i) {
+  const int e = p.ids[i] - p.e0;
+  return (e >= 0 && e < p.n_local) ? e : -1;
+}
+
+__global__ __launch_bounds__(kChunk) void count_kernel(IndexKParams p) {
+  extern __shared__ int h[];
+  for (int e = threadIdx.x; e < p.n_local; e += kChunk) h[e] = 0;
+  __syncthreads();
+  const int64_t i = (int64_t)blockIdx.x * kChunk + threadIdx.x;
+  if (i < (int64_t)p.T * p.topk) {
+    const int e = local_expert(p, i);
+    if (e >= 0) atomicAdd(&h[e], 1);
+  }
+  __syncthreads();
+  for (int e = threadIdx.x; e < p.n_local; e += kChunk) p.hist[(int64_t)e * p.nchunks + blockIdx.x] = h[e];
+}
+
+// Block-wide exclusive scan of one value per thread (NT threads), total out.
+template <int NT>
+__device__ int block_exclusive_scan(int v, int* s, int& total) {
+  const int t = threadIdx.x;
+  s[t] = v;
+  __syncthreads();
+  for (int off = 1; off < NT; off <<= 1) {
+    const int x = t >= off ? s[t - off] : 0;
+    __syncthreads();
+    s[t] += x;
+    __syncthreads();
+  }
+  total = s[NT - 1];
+  const int r = s[t] - v;
+  __syncthreads();
+  return r;
+}
+
+constexpr int kPlanThreads = 1024;
+
+__global__ __launch_bounds__(kPlanThreads) void plan_kernel(IndexKParams p) {
+  __shared__ int s[kPlanThreads];
+  __shared__ int carry;
+  // per expert: totals, and the exclusive prefix over chunks (in place)
+  for (int e = threadIdx.x; e < p.n_local; e += kPlanThreads) {
+    int* h = p.hist + (int64_t)e * p.nchunks;
+    int run = 0;
+    for (int c = 0; c < p.nchunks; ++c) {
+      const int v = h[c];
+      h[c] = run;
+      run += v;
+    }
+    p.exp_cnt[e] = run;
+  }
+  __syncthreads();
+  // padded expert offsets: exclusive scan over experts, kPlanThreads at a time
+  if (threadIdx.x == 0) carry = 0;
+  __syncthreads();
+  int64_t routed = 0;
+  for (int e0 = 0; e0 < p.n_local; e0 += kPlanThreads) {
+    const int e = e0 + threadIdx.x;
+    const int cnt = e < p.n_local ? p.exp_cnt[e] : 0;
+    const int padded = (cnt + p.row_block - 1) / p.row_block * p.row_block;
+    int tot;
+    const int ex = block_exclusive_scan<kPlanThreads>(padded, s, tot);
+    if (e < p.n_local) {
+      p.exp_off[e] = carry + ex;
+      if (p.out.padded_tokens_per_expert) p.out.padded_tokens_per_expert[e] = padded;
+      if (p.out.local_rb_per_expert) p.out.local_rb_per_expert[e] = cnt / p.row_block;
+    }
+    int rtot;
+    block_exclusive_scan<kPlanThreads>(cnt, s, rtot);
+    routed += rtot;
+    __syncthreads();
+    if (threadIdx.x == 0) carry += tot;
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    p.exp_off[p.n_local] = carry;
+    p.sizes[0] = routed;
+    p.sizes[1] = carry;
+  }
+  __syncthreads();
+  // chunk prefixes become absolute row bases
+  for (int e = threadIdx.x; e < p.n_local; e += kPlanThreads) {
+    int* h = p.hist + (int64_t)e * p.nchunks;
+    const int off = p.exp_off[e];
+    for (int c = 0; c < p.nchunks; ++c) h[c] += off;
+  }
+}
+
+__global__ __launch_bounds__(256) void tokens_kernel(IndexKParams p) {
+  const int t = blockIdx.x * 256 + threadIdx.x;
+  if (t >= p.T) return;
+  int c = 0;
+  for (int k = 0; k < p.topk; ++k) c += local_expert(p, (int64_t)t * p.topk + k) >= 0;
+  p.tok[t] = c;
+}
+
+__global__ __launch_bounds__(kPlanThreads) void offsets_kernel(IndexKParams p) {
+  __shared__ int s[kPlanThreads];
+  int carry = 0;
+  for (int t0 = 0; t0 < p.T; t0 += kPlanThreads) {
+    const int t = t0 + threadIdx.x;
+    const int v = t < p.T ? p.tok[t] : 0;
+    int tot;
+    const int ex = block_exclusive_scan<kPlanThreads>(v, s, tot);
+    if (t < p.T && p.out.owner_offset) p.out.owner_offset[t] = carry + ex;
+    carry += tot;
+  }
+  if (threadIdx.x == 0 && p.out.owner_offset) p.out.owner_offset[p.T] = carry;
+}
+
+__global__ __launch_bounds__(kChunk) void scatter_kernel(IndexKParams p) {
+  __shared__ int ex[kChunk];
+  const int64_t i = (int64_t)blockIdx.x * kChunk + threadIdx.x;
+  const bool in = i < (int64_t)p.T * p.topk;
+  const int e = in ? local_expert(p, i) : -1;
+  ex[threadIdx.x] = e;
+  __syncthreads();
+  if (e < 0) return;
+  // stable rank among this chunk's earlier entries of the same expert
+  int rank = 0;
+  for (int j = 0; j < (int)threadIdx.x; ++j) rank += ex[j] == e;
+  const int64_t row = (int64_t)p.hist[(int64_t)e * p.nchunks + blockIdx.x] + rank;
+  const int t = (int)(i / p.topk), k = (int)(i % p.topk);
+  // slot: the token's routed entries in row order = (expert, k) order
+  int before = 0;
+  for (int k2 = 0; k2 < p.topk; ++k2) {
+    const int e2 = local_expert(p, (int64_t)t * p.topk + k2);
+    before += e2 >= 0 && (e2 < e || (e2 == e && k2 < k));
+  }
+  if (row >= p.cap) return;  // capacity exceeded: sizes reports R_pad > cap
+  const mk_moe_index& o = p.out;
+  if (o.pull_indices) {
+    o.pull_indices[3 * row + 0] = 0;
+    o.pull_indices[3 * row + 1] = 0;
+    o.pull_indices[3 * row + 2] = t;
+  }
+  if (o.row_weight) o.row_weight[row] = p.gates[i];
+  if (o.row_to_owner) o.row_to_owner[row] = 0;
+  if (o.owner_offset) {
+    const int slot = o.owner_offset[t] + before;
+    if (o.row_to_slot) o.row_to_slot[row] = slot;
+    if (o.slot_to_row) o.slot_to_row[slot] = (int32_t)row;
+  }
+}
+
+__global__ __launch_bounds__(256) void pad_kernel(IndexKParams p) {
+  const int64_t r = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t R_pad = p.sizes[1];
+  if (r >= R_pad || r >= p.cap) return;
+  // expert of row r: last e with exp_off[e] <= r (binary search)
+  int lo = 0, hi = p.n_local - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) / 2;
+    if (p.exp_off[mid] <= r) lo = mid;
+    else hi = mid - 1;
+  }
+  const int e = lo;
+  const int64_t i = r - p.exp_off[e];
+  const int cnt = p.exp_cnt[e];
+  const mk_moe_index& o = p.out;
+  if (o.row_expert) o.row_expert[r] = e;
+  if (i >= cnt) {
+    if (o.pull_indices) {
+      o.pull_indices[3 * r + 0] = -1;
+      o.pull_indices[3 * r + 1] = -1;
+      o.pull_indices[3 * r + 2] = -1;
+    }
+    if (o.row_weight) o.row_weight[r] = 0.f;
+    if (o.row_to_slot) o.row_to_slot[r] = 0;
+    if (o.row_to_owner) o.row_to_owner[r] = -1;
+  }
+  if (r % p.row_block == 0) {
+    const int64_t b = r / p.row_block;
+    if (o.rb_expert) o.rb_expert[b] = e;
+    if (o.rb_rows) o.rb_rows[b] = (int)max((int64_t)0, min((int64_t)p.row_block, (int64_t)cnt - i));
+  }
+}
+
+int64_t index_workspace_bytes(int T, int topk, int n_local) {
+  const int64_t nchunks = ((int64_t)T * topk + kChunk - 1) / kChunk;
+  const int64_t ints = (int64_t)n_local * (nchunks > 0 ? nchunks : 1) + 2 * (int64_t)n_local + 1 + T;
+  return (ints * 4 + 255) / 256 * 256;
+}
+
+hipError_t launch_build_indices(const int32_t* ids, const float* gates, int T, int topk, int e0, int n_local,
+                                int row_block, int64_t cap, void* ws, int64_t* sizes, const mk_moe_index& out,
+                                hipStream_t stream) {
+  IndexKParams p;
+  p.ids = ids;
+  p.gates = gates;
+  p.T = T; p.topk = topk; p.e0 = e0; p.n_local = n_local; p.row_block = row_block;
+  p.cap = cap;
+  p.nchunks = (int)(((int64_t)T * topk + kChunk - 1) / kChunk);
+  const int nch = p.nchunks > 0 ? p.nchunks : 1;
+  int* w = static_cast<int*>(ws);
+  p.hist = w;
+  p.exp_off = w + (int64_t)n_local * nch;
+  p.exp_cnt = p.exp_off + n_local + 1;
+  p.tok = p.exp_cnt + n_local;
+  p.sizes = sizes;
+  p.out = out;
+  // (no routed entries: plan sees nchunks = 0 and empty experts)
+  if (p.nchunks > 0)
+    hipLaunchKernelGGL(count_kernel, dim3(p.nchunks), dim3(kChunk), n_local * sizeof(int), stream, p);
+  hipLaunchKernelGGL(plan_kernel, dim3(1), dim3(kPlanThreads), 0, stream, p);
+  if (T > 0) hipLaunchKernelGGL(tokens_kernel, dim3((T + 255) / 256), dim3(256), 0, stream, p);
+  hipLaunchKernelGGL(offsets_kernel, dim3(1), dim3(kPlanThreads), 0, stream, p);
+  if (p.nchunks > 0) hipLaunchKernelGGL(scatter_kernel, dim3(p.nchunks), dim3(kChunk), 0, stream, p);
+  if (cap > 0) hipLaunchKernelGGL(pad_kernel, dim3((unsigned)((cap + 255) / 256)), dim3(256), 0, stream, p);
+  return hipGetLastError();
+}
+
+}  // namespace mk

@@ -13,7 +13,7 @@ import torch
 
 from . import capi
 from .capi import (AgGemmArgs, GemmArgs, GemmRsArgs, MoeCombineArgs, MoeFfnArgs, MoeGroupedGemmArgs,
-                   MoeIndex, MoePermuteArgs)
+                   MoeIndex, MoeIndexDevArgs, MoePermuteArgs)
 
 
 def _ptr(t: torch.Tensor | None) -> int | None:
@@ -135,6 +135,58 @@ def moe_build_indices(topk_ids: np.ndarray, gates: np.ndarray, e0: int, n_local:
     o["slot_to_row"] = o["slot_to_row"][:R]
     o["R"], o["R_pad"] = R, Rp
     return o
+
+
+_INDEX_TABLES = ("padded_tokens_per_expert", "local_rb_per_expert", "pull_indices", "row_expert", "rb_expert",
+                 "rb_rows", "row_weight", "owner_offset", "row_to_slot", "row_to_owner", "slot_to_row")
+
+
+def moe_build_indices_dev(topk_ids: torch.Tensor, gates: torch.Tensor, e0: int, n_local: int,
+                          row_block: int = capi.ROW_BLOCK, sync: bool = True) -> dict:
+    """Routing index build on the GPU (mk_moe_build_indices_dev) from device
+    top-k ids (int32) and gates (float32) [T, k].  Tables are allocated at
+    the worst-case capacity; with sync=True the sizes are read back and the
+    returned tensors are views trimmed to R / R_pad rows (the same dict
+    layout as moe_build_indices, as device tensors)."""
+    if topk_ids.dtype != torch.int32 or gates.dtype != torch.float32 or not topk_ids.is_cuda:
+        raise ValueError("topk_ids must be int32 and gates float32 device tensors")
+    ids = topk_ids.contiguous()
+    g = gates.contiguous()
+    T, k = ids.shape
+    dev = ids.device
+    cap = T * k + n_local * (row_block - 1)
+    i32 = dict(dtype=torch.int32, device=dev)
+    t = {
+        "padded_tokens_per_expert": torch.empty(n_local, **i32),
+        "local_rb_per_expert": torch.empty(n_local, **i32),
+        "pull_indices": torch.empty((cap, 3), **i32),
+        "row_expert": torch.empty(cap, **i32),
+        "rb_expert": torch.empty((cap + row_block - 1) // row_block, **i32),
+        "rb_rows": torch.empty((cap + row_block - 1) // row_block, **i32),
+        "row_weight": torch.empty(cap, dtype=torch.float32, device=dev),
+        "owner_offset": torch.empty(T + 1, **i32),
+        "row_to_slot": torch.empty(cap, **i32),
+        "row_to_owner": torch.empty(cap, **i32),
+        "slot_to_row": torch.empty(max(cap, 1), **i32),
+    }
+    L = capi.lib()
+    wsb = int(L.mk_moe_index_workspace_bytes(T, k, n_local))
+    ws = torch.empty(max(wsb, 4), dtype=torch.uint8, device=dev)
+    sizes = torch.zeros(2, dtype=torch.int64, device=dev)
+    idx = MoeIndex(*[_ptr(t[f]) for f, _ in MoeIndex._fields_])
+    args = MoeIndexDevArgs(_ptr(ids), _ptr(g), T, k, e0, n_local, row_block, cap, _ptr(ws), wsb, _ptr(sizes), idx)
+    capi.call("mk_moe_build_indices_dev", args, _stream())
+    if not sync:
+        t["sizes"] = sizes
+        return t
+    R, Rp = (int(v) for v in sizes.cpu())
+    for f in ("pull_indices", "row_expert", "row_weight", "row_to_slot", "row_to_owner"):
+        t[f] = t[f][:Rp]
+    t["rb_expert"] = t["rb_expert"][:Rp // row_block]
+    t["rb_rows"] = t["rb_rows"][:Rp // row_block]
+    t["slot_to_row"] = t["slot_to_row"][:R]
+    t["R"], t["R_pad"] = R, Rp
+    return t
 
 
 def moe_permute(tokens, pull, post, tokens_per_src: int | None = None, devs_per_node: int = 1):

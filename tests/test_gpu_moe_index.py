@@ -1,0 +1,96 @@
+"""GPU routing-index build (mk_moe_build_indices_dev) against the host
+builder mk_moe_build_indices, table by table and bit for bit.  The host
+builder is itself pinned to the oracle's restatements of the reference's
+Python builders (tests/test_capi_host.py, tests/test_oracle.py)."""
+import numpy as np
+import pytest
+import torch
+
+from mkernel_amd import ops, workloads as wl
+
+pytestmark = pytest.mark.gpu
+
+TABLES = ("padded_tokens_per_expert", "local_rb_per_expert", "pull_indices", "row_expert", "rb_expert", "rb_rows",
+          "row_weight", "owner_offset", "row_to_slot", "row_to_owner", "slot_to_row")
+
+
+def _say(msg):
+    print(msg, flush=True)
+
+
+def _check(dev, ids, gates, e0, n_local, row_block=128):
+    ids = np.ascontiguousarray(ids, dtype=np.int32)
+    gates = np.ascontiguousarray(gates, dtype=np.float32)
+    host = ops.moe_build_indices(ids, gates, e0, n_local, row_block)
+    gpu = ops.moe_build_indices_dev(torch.from_numpy(ids).to(dev), torch.from_numpy(gates).to(dev), e0, n_local,
+                                    row_block)
+    assert (gpu["R"], gpu["R_pad"]) == (host["R"], host["R_pad"])
+    for f in TABLES:
+        h = np.asarray(host[f])
+        g = gpu[f].cpu().numpy()
+        assert g.shape == h.shape, f
+        assert np.array_equal(g.view(np.uint32) if g.dtype == np.float32 else g,
+                              h.view(np.uint32) if h.dtype == np.float32 else h), f
+    return host
+
+
+def test_index_dev_baseline_routing(dev):
+    """BASELINE configs 4/5 routing: 4096 tokens, top-8 of 256 (Zipf 1.1),
+    rank 0 of 8 owns experts 0-31."""
+    _say("moe index dev baseline")
+    cfg = wl.MoeCfg()
+    ids, gates = wl.zipf_routing(cfg.tokens, cfg.experts, cfg.topk, cfg.zipf_s, 6)  # moe_inputs' routing (seed 0)
+    host = _check(dev, ids, gates, cfg.e0, cfg.n_local)
+    assert host["R"] == 3528 and host["R_pad"] == 6016
+
+
+@pytest.mark.parametrize("rank", [0, 1, 7])
+def test_index_dev_small(dev, rank):
+    _say(f"moe index dev small rank={rank}")
+    cfg = wl.MoeCfg(tokens=512, H=512, I=256, experts=64, topk=8, ep=8, rank=rank)
+    ids, gates = wl.zipf_routing(cfg.tokens, cfg.experts, cfg.topk, cfg.zipf_s, 6)
+    _check(dev, ids, gates, cfg.e0, cfg.n_local)
+
+
+def test_index_dev_edge_cases(dev):
+    _say("moe index dev edge cases")
+    rng = np.random.default_rng(5)
+    # no routed entries at all
+    ids = np.full((37, 4), 99, np.int32)
+    host = _check(dev, ids, rng.random((37, 4)), 0, 8)
+    assert host["R"] == 0 and host["R_pad"] == 0
+    # one token; duplicates of a local expert inside a token; all to one expert
+    _check(dev, np.array([[3, 1, 3, 7]]), rng.random((1, 4)), 0, 8)
+    _check(dev, np.array([[2, 2, 5, 2], [2, 0, 2, 9]]), rng.random((2, 4)), 0, 8)
+    _check(dev, np.full((300, 2), 6), rng.random((300, 2)), 0, 8)
+    # entry count not a multiple of the 256-entry chunk; experts offset; row_block 64
+    ids = rng.integers(0, 40, size=(1001, 3))
+    _check(dev, ids, rng.random((1001, 3)), 8, 16)
+    _check(dev, ids, rng.random((1001, 3)), 8, 16, row_block=64)
+    # more local experts than a plan block's threads
+    ids = rng.integers(0, 3000, size=(777, 9))
+    _check(dev, ids, rng.random((777, 9)), 100, 1500)
+
+
+def test_index_dev_feeds_ffn(dev):
+    """The device tables drive the fused FFN + combine exactly like the host
+    tables (same bytes in, same bytes out)."""
+    _say("moe index dev -> ffn")
+    cfg = wl.MoeCfg(tokens=256, H=512, I=256, experts=64, topk=8, ep=8, rank=0)
+    tokens, ids, gates, w1, w2 = wl.moe_inputs(cfg)
+    g = ops.moe_build_indices_dev(torch.from_numpy(np.ascontiguousarray(ids, np.int32)).to(dev),
+                                  torch.from_numpy(np.ascontiguousarray(gates, np.float32)).to(dev),
+                                  cfg.e0, cfg.n_local)
+    h = ops.moe_build_indices(ids, gates, cfg.e0, cfg.n_local)
+    hd = {k: torch.from_numpy(np.ascontiguousarray(v)).to(dev) for k, v in h.items() if isinstance(v, np.ndarray)}
+    outs = []
+    for d in (g, hd):
+        Rp = g["R_pad"]
+        post = torch.empty((Rp, cfg.H), dtype=torch.bfloat16, device=dev)
+        act = torch.empty((Rp, cfg.I), dtype=torch.bfloat16, device=dev)
+        ye = torch.empty((Rp, cfg.H), dtype=torch.bfloat16, device=dev)
+        y = torch.empty((cfg.tokens, cfg.H), dtype=torch.float32, device=dev)
+        ops.moe_ffn_combine(tokens.to(dev), d["pull_indices"], d["row_weight"], d["owner_offset"], d["slot_to_row"],
+                            w1.to(dev), w2.to(dev), post, act, ye, y, rb_expert=d["rb_expert"], rb_rows=d["rb_rows"])
+        outs.append(y.cpu())
+    assert torch.equal(outs[0], outs[1])
