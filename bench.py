@@ -158,11 +158,14 @@ def bench_moe(steps, warmup, extra):
     y = torch.empty((cfg.tokens, cfg.H), dtype=torch.bfloat16, device="cuda")
     t = Timer()
 
-    def dispatch_gemm(i):
+    def dispatch_gemm_unfused(i):
         ops.moe_permute(tokens, d["pull_indices"], post)
         ops.moe_grouped_gemm(post, w1, h, rb_expert=d["rb_expert"], mode=0, rb_rows=d["rb_rows"])
 
-    ms4 = t.run(dispatch_gemm, steps, warmup)
+    # config 4: dispatch fused into GEMM1 (rows gathered through the pull table)
+    ms4 = t.run(lambda i: ops.moe_grouped_gemm(tokens, w1, h, rb_expert=d["rb_expert"], mode=0, rb_rows=d["rb_rows"],
+                                               gather_pull=d["pull_indices"]), steps, warmup)
+    ms4_unfused = t.run(dispatch_gemm_unfused, steps, warmup)
     ms_perm = t.run(lambda i: ops.moe_permute(tokens, d["pull_indices"], post), steps, warmup)
     ms_g1 = t.run(lambda i: ops.moe_grouped_gemm(post, w1, act, rb_expert=d["rb_expert"], mode=1,
                                                  rb_rows=d["rb_rows"]), steps, warmup)
@@ -170,10 +173,15 @@ def bench_moe(steps, warmup, extra):
                                                  rb_rows=d["rb_rows"]), steps, warmup)
     ms_comb = t.run(lambda i: ops.moe_combine(ye, d["row_weight"], d["owner_offset"], d["slot_to_row"], y),
                     steps, warmup)
-    ms5 = t.run(lambda i: ops.moe_ffn_combine(tokens, d["pull_indices"], d["row_weight"], d["owner_offset"],
-                                              d["slot_to_row"], w1, w2, post, act, ye, y, rb_expert=d["rb_expert"],
-                                              rb_rows=d["rb_rows"]),
-                steps, warmup)
+    def ffn(fuse):
+        return lambda i: ops.moe_ffn_combine(tokens, d["pull_indices"], d["row_weight"], d["owner_offset"],
+                                             d["slot_to_row"], w1, w2, post, act, ye, y, rb_expert=d["rb_expert"],
+                                             rb_rows=d["rb_rows"], fuse_dispatch=fuse)
+
+    # config 5: the layer with the dispatch fused into GEMM1 (the headline),
+    # and with the separate permute kernel
+    r5 = interleaved({"fused": ffn(True), "unfused": ffn(False)}, steps, warmup)
+    ms5, ms5_unfused = r5["fused"], r5["unfused"]
     # routing index build on the GPU (tables from device top-k ids / gates)
     ids_np, gates_np = wl.zipf_routing(cfg.tokens, cfg.experts, cfg.topk, cfg.zipf_s, 6)
     ids_d = torch.from_numpy(np.ascontiguousarray(ids_np, np.int32)).cuda()
@@ -190,9 +198,11 @@ def bench_moe(steps, warmup, extra):
     f5 = 6.0 * R * cfg.H * cfg.I
     layer_bytes = w_bytes1 + w_bytes2 + 2 * R_pad * cfg.H * 2 * 2 + R_pad * cfg.I * 2 * 2 + cfg.tokens * cfg.H * 4
     extra["moe_dispatch_gemm1"] = {"R": R, "R_pad": R_pad, "experts_used": int(used.sum()), "us": ms4 * 1e3,
-                                   "tflops": f4 / ms4 / 1e9, "us_permute": ms_perm * 1e3,
+                                   "tflops": f4 / ms4 / 1e9, "us_permute_then_gemm1": ms4_unfused * 1e3,
+                                   "us_permute": ms_perm * 1e3,
                                    "permute_GBs": 2 * R_pad * cfg.H * 2 / ms_perm / 1e6}
     extra["moe_ffn_combine"] = {"us": ms5 * 1e3, "tokens_per_s": cfg.tokens / ms5 * 1e3, "tflops": f5 / ms5 / 1e9,
+                                "us_with_separate_permute": ms5_unfused * 1e3,
                                 "frac_peak": f5 / ms5 / 1e9 / PEAK_BF16_TFLOPS,
                                 "hbm_bound_GBs": layer_bytes / ms5 / 1e6,
                                 "us_gemm1_swiglu": ms_g1 * 1e3, "us_gemm2": ms_g2 * 1e3, "us_combine": ms_comb * 1e3,

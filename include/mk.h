@@ -229,6 +229,15 @@ typedef struct mk_moe_grouped_gemm_args {
   int32_t num_cus;
   void* split_ws;              /* optional K-split workspace, as in mk_gemm_args */
   int64_t split_ws_bytes;
+  /* Fused dispatch (the reference's moe_dispatch_gemm_fused,
+   * include/operators/dispatch_gemm/dispatch_gemm.cuh:238-262): when
+   * gather_pull is set, A is the token buffer [n_src_rows, K] and GEMM row r
+   * reads token row (src_node * devs_per_node + src_dev) * tokens_per_src +
+   * src_token of pull row r (padding rows read zeros); no permuted copy is
+   * made.  n_src_rows * K * 2 must stay below 2 GiB. */
+  const int32_t* gather_pull;  /* [R_pad, 3] device, or NULL */
+  int64_t n_src_rows;
+  int32_t tokens_per_src, devs_per_node;
 } mk_moe_grouped_gemm_args;
 int mk_moe_grouped_gemm(const mk_moe_grouped_gemm_args* args, void* stream);
 
@@ -285,6 +294,7 @@ typedef struct mk_moe_ffn_args {
   int32_t num_cus;
   void* split_ws;              /* optional K-split workspace, as in mk_gemm_args */
   int64_t split_ws_bytes;
+  int32_t fuse_dispatch;       /* 1: GEMM1 gathers tokens itself, post_tokens is not written */
 } mk_moe_ffn_args;
 int mk_moe_ffn_combine(const mk_moe_ffn_args* args, void* stream);
 

@@ -91,7 +91,8 @@ class MoeGroupedGemmArgs(C.Structure):
     _fields_ = [("A", vp), ("W", vp), ("out", vp), ("rb_expert", vp), ("padded_tokens_per_expert", vp),
                 ("rb_rows", vp), ("R_pad", i64), ("K", i64),
                 ("Nw", i64), ("num_experts", i32), ("mode", i32), ("num_cus", i32), ("split_ws", vp),
-                ("split_ws_bytes", i64)]
+                ("split_ws_bytes", i64), ("gather_pull", vp), ("n_src_rows", i64), ("tokens_per_src", i32),
+                ("devs_per_node", i32)]
 
 
 class MoeCombineArgs(C.Structure):
@@ -106,7 +107,7 @@ class MoeFfnArgs(C.Structure):
                 ("act", vp), ("y_expert", vp), ("y_out", vp), ("num_tokens", i64), ("n_src_rows", i64),
                 ("R_pad", i64), ("H", i64), ("I", i64), ("num_experts", i32), ("tokens_per_src", i32),
                 ("devs_per_node", i32), ("out_dtype", i32), ("num_cus", i32), ("split_ws", vp),
-                ("split_ws_bytes", i64)]
+                ("split_ws_bytes", i64), ("fuse_dispatch", i32)]
 
 
 _lib = None

@@ -405,12 +405,17 @@ int mk_moe_permute(const mk_moe_permute_args* a, void* stream) {
 static int grouped_gemm_impl(const void* A, const void* W, void* out, const int32_t* rb_expert,
                              const int32_t* expert_rows, const int32_t* rb_rows, int64_t R_pad, int64_t K,
                              int64_t Nw, int32_t E, int32_t mode, int32_t num_cus, void* split_ws,
-                             int64_t split_ws_bytes, hipStream_t stream) {
+                             int64_t split_ws_bytes, const int32_t* gather_pull, int64_t n_src_rows,
+                             int32_t tokens_per_src, int32_t devs_per_node, hipStream_t stream) {
   if (!A || !W || !out || (!rb_expert && !expert_rows)) return fail(MK_EINVAL, "mk_moe_grouped_gemm: null argument");
   if (mode != 0 && mode != 1) return fail(MK_EINVAL, "mk_moe_grouped_gemm: mode must be 0 or 1");
   if (E <= 0) return fail(MK_EINVAL, "mk_moe_grouped_gemm: num_experts must be positive");
   if (R_pad == 0) return MK_OK;
   if (int rc = check_gemm_shape(R_pad, Nw, K, 128)) return rc;
+  if (gather_pull && (n_src_rows <= 0 || tokens_per_src <= 0 || devs_per_node <= 0 ||
+                      n_src_rows * K * 2 >= (1LL << 31)))
+    return fail(MK_EINVAL, "mk_moe_grouped_gemm: fused dispatch needs n_src_rows, tokens_per_src, devs_per_node "
+                           "> 0 and a token buffer below 2 GiB");
   DevInfo d;
   if (int rc = device_info(&d)) return rc;
   mk::GemmKParams p;
@@ -428,6 +433,10 @@ static int grouped_gemm_impl(const void* A, const void* W, void* out, const int3
   p.rb_rows = rb_rows;
   p.n_experts = E;
   p.swiglu_I = (int)(Nw / 2);
+  p.gather_pull = gather_pull;
+  p.gather_rows = n_src_rows;
+  p.gather_tps = tokens_per_src;
+  p.gather_devs = devs_per_node;
   const int total = num_cus > 0 ? num_cus : d.cus;
   set_grid(p, total, 0, p.tiles_m * p.tiles_n);
   if (int rc = check_ws(split_ws, split_ws_bytes, "mk_moe_grouped_gemm")) return rc;
@@ -439,7 +448,8 @@ static int grouped_gemm_impl(const void* A, const void* W, void* out, const int3
 int mk_moe_grouped_gemm(const mk_moe_grouped_gemm_args* a, void* stream) {
   if (!a) return fail(MK_EINVAL, "mk_moe_grouped_gemm: null argument");
   return grouped_gemm_impl(a->A, a->W, a->out, a->rb_expert, a->padded_tokens_per_expert, a->rb_rows, a->R_pad, a->K, a->Nw, a->num_experts, a->mode,
-                           a->num_cus, a->split_ws, a->split_ws_bytes, static_cast<hipStream_t>(stream));
+                           a->num_cus, a->split_ws, a->split_ws_bytes, a->gather_pull, a->n_src_rows,
+                           a->tokens_per_src, a->devs_per_node, static_cast<hipStream_t>(stream));
 }
 
 int mk_moe_combine(const mk_moe_combine_args* a, void* stream) {
@@ -501,16 +511,25 @@ int mk_moe_ffn_combine(const mk_moe_ffn_args* a, void* stream) {
   if (!a) return fail(MK_EINVAL, "mk_moe_ffn_combine: null argument");
   if (a->I % 128) return fail(MK_ESHAPE, "mk_moe_ffn_combine: I must be a multiple of 128");
   hipStream_t s = static_cast<hipStream_t>(stream);
-  mk_moe_permute_args pa{a->tokens, a->pull_indices, a->post_tokens, a->R_pad, a->H,
-                         a->n_src_rows, a->tokens_per_src, a->devs_per_node};
-  if (int rc = mk_moe_permute(&pa, stream)) return rc;
-  if (int rc = grouped_gemm_impl(a->post_tokens, a->w1, a->act, a->rb_expert, a->padded_tokens_per_expert,
-                                 a->rb_rows, a->R_pad,
-                                 a->H, 2 * a->I, a->num_experts, 1, a->num_cus, a->split_ws, a->split_ws_bytes, s))
-    return rc;
+  if (a->fuse_dispatch) {
+    if (!a->pull_indices) return fail(MK_EINVAL, "mk_moe_ffn_combine: null argument");
+    if (int rc = grouped_gemm_impl(a->tokens, a->w1, a->act, a->rb_expert, a->padded_tokens_per_expert, a->rb_rows,
+                                   a->R_pad, a->H, 2 * a->I, a->num_experts, 1, a->num_cus, a->split_ws,
+                                   a->split_ws_bytes, a->pull_indices, a->n_src_rows, a->tokens_per_src,
+                                   a->devs_per_node, s))
+      return rc;
+  } else {
+    mk_moe_permute_args pa{a->tokens, a->pull_indices, a->post_tokens, a->R_pad, a->H,
+                           a->n_src_rows, a->tokens_per_src, a->devs_per_node};
+    if (int rc = mk_moe_permute(&pa, stream)) return rc;
+    if (int rc = grouped_gemm_impl(a->post_tokens, a->w1, a->act, a->rb_expert, a->padded_tokens_per_expert,
+                                   a->rb_rows, a->R_pad, a->H, 2 * a->I, a->num_experts, 1, a->num_cus,
+                                   a->split_ws, a->split_ws_bytes, nullptr, 0, 0, 0, s))
+      return rc;
+  }
   if (int rc = grouped_gemm_impl(a->act, a->w2, a->y_expert, a->rb_expert, a->padded_tokens_per_expert,
-                                 a->rb_rows, a->R_pad,
-                                 a->I, a->H, a->num_experts, 0, a->num_cus, a->split_ws, a->split_ws_bytes, s))
+                                 a->rb_rows, a->R_pad, a->I, a->H, a->num_experts, 0, a->num_cus, a->split_ws,
+                                 a->split_ws_bytes, nullptr, 0, 0, 0, s))
     return rc;
   mk_moe_combine_args ca{a->y_expert, a->row_weight, a->owner_offset, a->slot_to_row, a->y_out,
                          a->num_tokens, a->H, a->out_dtype};

@@ -499,7 +499,14 @@ __device__ void compute_role(const GemmKParams& p, int cons_id, char* smem, cons
       __syncthreads();
     }
 
-    const u32x4_t rA = make_rsrc_v(p.A + (int64_t)m0 * p.lda, (uint32_t)(C::BM * p.lda * 2));
+    // Fused dispatch (grouped GEMMs with gather_pull): A rows are gathered
+    // from the token buffer through the pull table — row r of the tile reads
+    // token row (src_node * devs + src_dev) * tokens_per_src + src_token;
+    // padding rows (src < 0) get an offset past the buffer's end, which the
+    // buffer load returns as zeros.
+    const u32x4_t rA = p.gather_pull
+                           ? make_rsrc_v(p.A, (uint32_t)(p.gather_rows * p.lda * 2))
+                           : make_rsrc_v(p.A + (int64_t)m0 * p.lda, (uint32_t)(C::BM * p.lda * 2));
     const u32x4_t rB = make_rsrc_v(Bp, (uint32_t)(p.K * p.ldb * 2));
     // DMA source offsets: lane l of a wave instruction fills LDS unit l of a
     // 1 KB block, i.e. (A) row 16*inst + l/4, unit l%4; (B) k-row 2*inst +
@@ -510,7 +517,13 @@ __device__ void compute_role(const GemmKParams& p, int cons_id, char* smem, cons
     for (int i = 0; i < C::A_INST; ++i) {
       const int row = (wave * C::A_INST + i) * 16 + (lane >> 2);
       const int c = (lane & 3) ^ ((row >> 2) & 3);
-      a_src[i] = (uint32_t)(row * p.lda * 2 + c * 16);
+      if (p.gather_pull) {
+        const int* pr = p.gather_pull + 3 * (int64_t)(m0 + row);
+        const int64_t srow = ((int64_t)pr[0] * p.gather_devs + pr[1]) * p.gather_tps + pr[2];
+        a_src[i] = (pr[0] < 0 || pr[2] < 0) ? 0x80000000u : (uint32_t)(srow * p.lda * 2 + c * 16);
+      } else {
+        a_src[i] = (uint32_t)(row * p.lda * 2 + c * 16);
+      }
     }
 #pragma unroll
     for (int i = 0; i < C::B_INST; ++i) {

@@ -31,6 +31,11 @@ struct GemmKParams {
   const int* rb_expert;
   const int* expert_rows;   // padded rows per expert (used when rb_expert is null)
   const int* rb_rows;       // real rows per 128-row tile (null: every row is real)
+  // fused dispatch: A is the token buffer [gather_rows, K], row r of the
+  // GEMM reads the token the pull table names (null: A rows are the rows)
+  const int* gather_pull;
+  int64_t gather_rows;
+  int gather_tps, gather_devs;
   int n_experts;
   // SwiGLU: width I of the gate half of B's columns
   int swiglu_I;

@@ -199,13 +199,18 @@ def moe_permute(tokens, pull, post, tokens_per_src: int | None = None, devs_per_
 
 
 def moe_grouped_gemm(A, W, out, rb_expert=None, padded_tokens_per_expert=None, mode: int = 0, num_cus: int = 0,
-                     rb_rows=None, split_ws=None):
+                     rb_rows=None, split_ws=None, gather_pull=None, tokens_per_src: int | None = None,
+                     devs_per_node: int = 1):
     """mode 0: out = A @ W[e]; mode 1: out = silu(h[:, :I]) * h[:, I:], h = A @ W[e]."""
     _bf16(A, "A"); _bf16(W, "W"); _bf16(out, "out")
-    R_pad, K = A.shape
+    # with gather_pull, A is the token buffer and the rows come from the pull table
+    R_pad = gather_pull.shape[0] if gather_pull is not None else A.shape[0]
+    K = A.shape[1]
     E, _, Nw = W.shape
+    tps = A.shape[0] if tokens_per_src is None else tokens_per_src
     args = MoeGroupedGemmArgs(_ptr(A), _ptr(W), _ptr(out), _ptr(rb_expert), _ptr(padded_tokens_per_expert),
-                              _ptr(rb_rows), R_pad, K, Nw, E, mode, num_cus, *_ws(split_ws, A.device))
+                              _ptr(rb_rows), R_pad, K, Nw, E, mode, num_cus, *_ws(split_ws, A.device),
+                              _ptr(gather_pull), A.shape[0], tps, devs_per_node)
     capi.call("mk_moe_grouped_gemm", args, _stream())
     return out
 
@@ -236,17 +241,20 @@ def moe_combine(y_expert, row_weight, owner_offset, slot_to_row, y_out):
 
 def moe_ffn_combine(tokens, pull, row_weight, owner_offset, slot_to_row, w1, w2, post, act, y_expert, y_out,
                     rb_expert=None, padded_tokens_per_expert=None, tokens_per_src: int | None = None,
-                    devs_per_node: int = 1, num_cus: int = 0, rb_rows=None, split_ws=None):
-    """permute -> grouped GEMM1 + SwiGLU -> grouped GEMM2 -> combine."""
+                    devs_per_node: int = 1, num_cus: int = 0, rb_rows=None, split_ws=None,
+                    fuse_dispatch: bool = False):
+    """permute -> grouped GEMM1 + SwiGLU -> grouped GEMM2 -> combine.  With
+    fuse_dispatch, GEMM1 reads the token rows through the pull table itself
+    (no permute kernel, post may be None and is not written)."""
     T, H = y_out.shape
     E, _, I2 = w1.shape
-    R_pad = post.shape[0]
+    R_pad = pull.shape[0]
     od = 0 if y_out.dtype == torch.float32 else 1
     tps = tokens.shape[0] if tokens_per_src is None else tokens_per_src
     args = MoeFfnArgs(_ptr(tokens), _ptr(pull), _ptr(rb_expert), _ptr(padded_tokens_per_expert), _ptr(rb_rows),
                       _ptr(row_weight),
                       _ptr(owner_offset), _ptr(slot_to_row), _ptr(w1), _ptr(w2), _ptr(post), _ptr(act), _ptr(y_expert),
                       _ptr(y_out), T, tokens.shape[0], R_pad, H, I2 // 2, E, tps, devs_per_node, od, num_cus,
-                      *_ws(split_ws, tokens.device))
+                      *_ws(split_ws, tokens.device), int(fuse_dispatch))
     capi.call("mk_moe_ffn_combine", args, _stream())
     return y_out

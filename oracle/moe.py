@@ -144,13 +144,25 @@ def build_indices_np(topk_ids: np.ndarray, gates: np.ndarray, e0: int, n_local: 
     }
 
 
-def permute_ref(tokens: torch.Tensor, pull: np.ndarray | torch.Tensor) -> torch.Tensor:
-    """post[r] = tokens[pull[r,2]] (bit-exact), zero rows for padding."""
+def permute_ref(tokens: torch.Tensor, pull: np.ndarray | torch.Tensor, tokens_per_src: int | None = None,
+                devs_per_node: int = 1) -> torch.Tensor:
+    """post[r] = tokens[src_row(r)] (bit-exact), zero rows for padding.
+
+    With one source (the default) src_row = src_token, as the reference's
+    single-rank benches build it.  Several sources are flattened into one
+    buffer of tokens_per_src rows each: src_row = (src_node * devs_per_node +
+    src_dev) * tokens_per_src + src_token — this build's layout for the
+    reference's per-device pre_tokens / peer_tokens views
+    (src/dispatch_gemm.cu:125-168)."""
     pull = torch.as_tensor(np.asarray(pull)).long()
     tokens = tokens.cpu()
     out = torch.zeros((pull.shape[0], tokens.shape[1]), dtype=tokens.dtype)
-    valid = pull[:, 0] >= 0
-    out[valid] = tokens[pull[valid, 2]]
+    valid = (pull[:, 0] >= 0) & (pull[:, 2] >= 0)
+    if tokens_per_src is None:
+        rows = pull[valid, 2]
+    else:
+        rows = (pull[valid, 0] * devs_per_node + pull[valid, 1]) * tokens_per_src + pull[valid, 2]
+    out[valid] = tokens[rows]
     return out
 
 

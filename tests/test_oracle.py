@@ -131,6 +131,16 @@ def test_permute_ref():
     assert torch.equal(out[0], tok[3]) and torch.equal(out[2], tok[9]) and (out[1] == 0).all()
 
 
+def test_permute_ref_multi_source_hand_example():
+    """Flattened sources: 2 nodes x 2 devs x 5 tokens; (1, 0, 2) is row
+    (1*2 + 0)*5 + 2 = 12, (0, 1, 4) is row 9."""
+    tok = wl.randn_bf16((20, 8), 2)
+    pull = np.array([[1, 0, 2], [0, 1, 4], [-1, -1, -1], [1, 1, 0]], np.int32)
+    out = om.permute_ref(tok, pull, tokens_per_src=5, devs_per_node=2)
+    assert torch.equal(out[0], tok[12]) and torch.equal(out[1], tok[9]) and (out[2] == 0).all()
+    assert torch.equal(out[3], tok[15])
+
+
 def test_silu_identities():
     x = torch.linspace(-20, 20, 401)
     one = torch.ones_like(x)
