@@ -163,9 +163,10 @@ def bench_moe(steps, warmup, extra):
         ops.moe_grouped_gemm(post, w1, h, rb_expert=d["rb_expert"], mode=0, rb_rows=d["rb_rows"])
 
     # config 4: dispatch fused into GEMM1 (rows gathered through the pull table)
-    ms4 = t.run(lambda i: ops.moe_grouped_gemm(tokens, w1, h, rb_expert=d["rb_expert"], mode=0, rb_rows=d["rb_rows"],
-                                               gather_pull=d["pull_indices"]), steps, warmup)
-    ms4_unfused = t.run(dispatch_gemm_unfused, steps, warmup)
+    r4 = interleaved({"fused": lambda i: ops.moe_grouped_gemm(tokens, w1, h, rb_expert=d["rb_expert"], mode=0,
+                                                              rb_rows=d["rb_rows"], gather_pull=d["pull_indices"]),
+                      "unfused": dispatch_gemm_unfused}, steps, warmup)
+    ms4, ms4_unfused = r4["fused"], r4["unfused"]
     ms_perm = t.run(lambda i: ops.moe_permute(tokens, d["pull_indices"], post), steps, warmup)
     ms_g1 = t.run(lambda i: ops.moe_grouped_gemm(post, w1, act, rb_expert=d["rb_expert"], mode=1,
                                                  rb_rows=d["rb_rows"]), steps, warmup)
