@@ -140,6 +140,34 @@ def bench_rs(steps, warmup, producers, extra):
                         "epilogue_bytes_read": peers.numel() * 2}
 
 
+def bench_ar(steps, warmup, producers, extra):
+    """GEMM + all-reduce at one rank's share (no BASELINE config: the config-3
+    down-projection at half the rows, 8192x8192x3584, 7 staged full peer
+    partials of 8192x8192 bf16 N(0,0.5))."""
+    M, N, K, world = 8192, 8192, 3584, 8
+    A = wl.randn_bf16((M, K), 60, K ** -0.5, "cuda")
+    B = wl.randn_bf16((K, N), 61, K ** -0.5, "cuda")
+    peers = wl.randn_bf16((world - 1, M, N), 62, 0.5, "cuda")
+    recv = torch.empty_like(peers)
+    nflags = (world - 1) * M // 128
+    flags = torch.zeros(nflags, dtype=torch.int32, device="cuda")
+    counters = torch.zeros_like(flags)
+    done = torch.zeros((M // 256) * (N // 256), dtype=torch.int32, device="cuda")
+    order = torch.from_numpy(wl.stage_order(nflags, 7)).cuda()
+    C = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+    epoch = [0]
+
+    def ar(i):
+        epoch[0] += 1
+        ops.gemm_ar(A, B, C, peers, recv, world, flags, order, epoch=epoch[0], num_producers=producers,
+                    stage_counters=counters, done_flags=done)
+
+    r = interleaved({"ar": ar, "plain": lambda i: ops.gemm(A, B, C)}, steps, warmup)
+    flops = 2.0 * M * N * K
+    extra["gemm_ar"] = {"shape": [M, N, K], "us": r["ar"] * 1e3, "tflops": flops / r["ar"] / 1e9,
+                        "us_plain_gemm_same_shape": r["plain"] * 1e3, "staged_bytes": peers.numel() * 2}
+
+
 def moe_setup(cfg: wl.MoeCfg):
     tokens, ids, gates, w1, w2 = wl.moe_inputs(cfg, device="cuda")
     idx = ops.moe_build_indices(ids, gates, cfg.e0, cfg.n_local)
@@ -249,7 +277,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--producers", type=int, default=-1,
                     help="-1: cooperative staging by every workgroup; >0: dedicated producer workgroups")
-    ap.add_argument("--workload", default="all", choices=["all", "ag", "gemm", "rs", "moe", "calib"])
+    ap.add_argument("--workload", default="all", choices=["all", "ag", "gemm", "rs", "ar", "moe", "calib"])
     ap.add_argument("--no-cpu", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -288,6 +316,10 @@ def main():
     if args.workload in ("all", "rs"):
         log("[bench] gemm_rs config 3")
         bench_rs(K, W, args.producers, extra)
+        torch.cuda.empty_cache()
+    if args.workload in ("all", "ar"):
+        log("[bench] gemm_ar (8192x8192x3584, 7 staged peer partials)")
+        bench_ar(K, W, args.producers, extra)
         torch.cuda.empty_cache()
     if args.workload in ("all", "moe"):
         log("[bench] moe configs 4/5")

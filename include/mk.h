@@ -134,6 +134,44 @@ typedef struct mk_gemm_rs_args {
 int mk_gemm_rs(const mk_gemm_rs_args* args, void* stream);
 
 /* ------------------------------------------------------------------------ */
+/* GEMM + all-reduce at one rank's share.
+ *   C_final = bf16( A @ B + sum_{p < world-1} peer_recv[p] )   (fp32 adds, p ascending)
+ * over all M rows: the reduce epilogue of mk_gemm_rs with every row owned.
+ * The producer role (or cooperative staging, num_producers = -1) copies
+ * peer_src into peer_recv in 128-row blocks, flags[(p * M/128) + block] =
+ * epoch, in the order stage_order; compute follows the arrival order of each
+ * row tile's last peer block.  When done_flags is set, each finished
+ * 256x256 output tile t = row_tile * (N/256) + col_tile is published as
+ * done_flags[t] = epoch after its bytes are visible at agent scope (the hand-off
+ * the reference's broadcast step reads).
+ * Replaces gemm_ar_multinode::entrypoint
+ * (reference include/operators/gemm_ar/session.cuh:188-215,
+ * src/gemm_ar.cu:1-33 compute + intra-AR roles; the reference checks
+ * C_final against all_reduce(matmul), bench/gemm_ar_bench.py:510-514). */
+typedef struct mk_gemm_ar_args {
+  const void* A;          /* bf16 [M, K] */
+  const void* B;          /* bf16 [K, N] */
+  void* C_final;          /* bf16 [M, N] */
+  const void* peer_src;   /* bf16 [world-1, M, N] partials to stage */
+  void* peer_recv;        /* bf16 [world-1, M, N] staged partials */
+  int64_t M, N, K;
+  int32_t world;
+  uint32_t* flags;              /* [(world-1) * M/128] */
+  const int32_t* stage_order;   /* [(world-1) * M/128]; NULL = ascending, no arrival order */
+  uint32_t epoch;
+  int32_t gated;
+  int32_t num_producers;        /* as in mk_ag_gemm (-1 = cooperative staging) */
+  int32_t num_cus;
+  uint32_t spin_limit;
+  uint32_t* error_word;
+  uint32_t* stage_counters;     /* [(world-1) * M/128] for producers == -1 */
+  uint32_t* done_flags;         /* [(M/256) * (N/256)] or NULL */
+  void* split_ws;
+  int64_t split_ws_bytes;
+} mk_gemm_ar_args;
+int mk_gemm_ar(const mk_gemm_ar_args* args, void* stream);
+
+/* ------------------------------------------------------------------------ */
 /* MoE routing index build (host memory, host CPU).  Restates the reference's
  * host-side builders bench/dispatch_gemm_bench.py:127-188 (build_routing,
  * build_pull_indices) and bench/dispatch_gemm_glu_combine_bench.py:222-293,

@@ -18,6 +18,7 @@ EXPORTS = (
     "mk_gemm",
     "mk_ag_gemm",
     "mk_gemm_rs",
+    "mk_gemm_ar",
     "mk_moe_index_sizes",
     "mk_moe_build_indices",
     "mk_moe_index_workspace_bytes",
@@ -68,6 +69,13 @@ class GemmRsArgs(C.Structure):
                 ("flags", vp), ("stage_order", vp), ("epoch", u32), ("gated", i32),
                 ("num_producers", i32), ("num_cus", i32), ("spin_limit", u32), ("error_word", vp),
                 ("stage_counters", vp), ("split_ws", vp), ("split_ws_bytes", i64)]
+
+
+class GemmArArgs(C.Structure):
+    _fields_ = [("A", vp), ("B", vp), ("C_final", vp), ("peer_src", vp), ("peer_recv", vp), ("M", i64), ("N", i64),
+                ("K", i64), ("world", i32), ("flags", vp), ("stage_order", vp), ("epoch", u32), ("gated", i32),
+                ("num_producers", i32), ("num_cus", i32), ("spin_limit", u32), ("error_word", vp),
+                ("stage_counters", vp), ("done_flags", vp), ("split_ws", vp), ("split_ws_bytes", i64)]
 
 
 class MoeIndex(C.Structure):
@@ -121,7 +129,7 @@ def lib() -> C.CDLL:
             raise RuntimeError(f"{LIB_PATH} is missing: run __graft_entry__.build() "
                                "(or python -m mkernel_amd._build) first")
         L = C.CDLL(str(LIB_PATH))
-        for name in ("mk_gemm", "mk_ag_gemm", "mk_gemm_rs", "mk_moe_permute", "mk_moe_grouped_gemm",
+        for name in ("mk_gemm", "mk_ag_gemm", "mk_gemm_rs", "mk_gemm_ar", "mk_moe_permute", "mk_moe_grouped_gemm",
                      "mk_moe_combine", "mk_moe_ffn_combine"):
             getattr(L, name).argtypes = [vp, vp]
             getattr(L, name).restype = C.c_int

@@ -300,6 +300,74 @@ int mk_gemm_rs(const mk_gemm_rs_args* a, void* stream) {
   return e == hipSuccess ? MK_OK : hip_fail(e, "mk_gemm_rs launch");
 }
 
+int mk_gemm_ar(const mk_gemm_ar_args* a, void* stream) {
+  if (!a || !a->A || !a->B || !a->C_final) return fail(MK_EINVAL, "mk_gemm_ar: null argument");
+  DevInfo d;
+  if (int rc = device_info(&d)) return rc;
+  const int bm = 256;
+  if (int rc = check_gemm_shape(a->M, a->N, a->K, bm)) return rc;
+  if (a->world < 1) return fail(MK_EINVAL, "mk_gemm_ar: world must be >= 1");
+  if (a->M / bm > mk::kMaxTilesM) return fail(MK_ESHAPE, "mk_gemm_ar: at most %d row tiles", mk::kMaxTilesM);
+  const int npeers = a->world - 1;
+  if (npeers > 0 && !a->peer_recv) return fail(MK_EINVAL, "mk_gemm_ar: peer_recv is null");
+  const int64_t nflags = (int64_t)npeers * (a->M / 128);
+  if (a->stage_order && nflags + a->M / bm > 8192)
+    return fail(MK_ESHAPE, "mk_gemm_ar: too many flags for the arrival-order schedule");
+  const int total = a->num_cus > 0 ? a->num_cus : d.cus;
+  if (a->num_producers < -1) return fail(MK_EINVAL, "mk_gemm_ar: num_producers must be >= -1");
+  const bool gated = a->gated && npeers > 0;
+  const bool coop = gated && a->num_producers == -1;
+  const int n_prod = (gated && a->num_producers > 0) ? a->num_producers : 0;
+  if (gated) {
+    if (!a->flags) return fail(MK_EINVAL, "mk_gemm_ar: gated launch needs flags");
+    if (a->num_producers != 0 && !a->peer_src) return fail(MK_EINVAL, "mk_gemm_ar: staging needs peer_src");
+    if (coop && !a->stage_counters) return fail(MK_EINVAL, "mk_gemm_ar: cooperative staging needs stage_counters");
+  }
+  if ((gated || a->done_flags) && a->epoch == 0) return fail(MK_EINVAL, "mk_gemm_ar: epoch 0 is reserved");
+  if (n_prod >= total) return fail(MK_EINVAL, "mk_gemm_ar: bad num_producers");
+  mk::GemmKParams p;
+  fill_common(p);
+  p.A = static_cast<const uint16_t*>(a->A);
+  p.B = static_cast<const uint16_t*>(a->B);
+  p.C = static_cast<uint16_t*>(a->C_final);  // every row is owned: rs_out
+  p.lda = a->K; p.ldb = a->N; p.ldc = a->N;
+  p.M = (int)a->M; p.N = (int)a->N; p.K = (int)a->K;
+  p.tiles_m = (int)(a->M / bm);
+  p.tiles_n = (int)(a->N / 256);
+  set_grid(p, total, n_prod, p.tiles_m * p.tiles_n);
+  p.rs_own_row0 = 0;
+  p.rs_own_rows = (int)a->M;
+  p.rs_npeers = npeers;
+  p.rs_recv = static_cast<const uint16_t*>(a->peer_recv);
+  p.rs_out = static_cast<uint16_t*>(a->C_final);
+  p.ar_done = a->done_flags;
+  p.epoch = a->epoch;
+  p.spin_limit = a->spin_limit;
+  p.err = a->error_word;
+  if (gated) {
+    p.rs_flags = a->flags;
+    if (a->stage_order) {
+      p.perm_mode = mk::kPermPeerArrival;
+      p.a_stage_order = a->stage_order;
+    }
+    if (n_prod > 0 || coop) {
+      p.st_src = static_cast<const uint16_t*>(a->peer_src);
+      p.st_dst = static_cast<uint16_t*>(a->peer_recv);
+      p.st_cols = (int)a->N;
+      p.st_nblocks = (int)nflags;
+      p.st_order = a->stage_order;
+      p.st_flags = a->flags;
+      p.st_counters = a->stage_counters;
+      p.st_coop = coop ? 1 : 0;
+      p.st_batch = 8;
+    }
+  }
+  if (int rc = check_ws(a->split_ws, a->split_ws_bytes, "mk_gemm_ar")) return rc;
+  plan_split(p, bm, a->split_ws, a->split_ws_bytes);
+  hipError_t e = mk::launch_gemm(p, bm, mk::kEpiReduce, static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? MK_OK : hip_fail(e, "mk_gemm_ar launch");
+}
+
 // ---------------------------------------------------------------------------
 // MoE
 // ---------------------------------------------------------------------------

@@ -35,6 +35,7 @@ namespace mk {
 
 typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t v2u32_t __attribute__((ext_vector_type(2)));
 
 // ---------------------------------------------------------------------------
 // Tile configuration
@@ -274,6 +275,14 @@ __device__ __forceinline__ void store_tile(const GemmKParams& p, f32x16 (&acc)[C
             w.y = pack_bf16x2(acc[i][j][4 * a + 2], acc[i][j][4 * a + 3]);
             *reinterpret_cast<uint2*>(orow + j * 32 + 8 * a) = w;
           }
+      }
+      if (p.ar_done) {
+        // all-reduce: publish the finished tile (the broadcast hand-off).
+        // The tile's 8-byte row pieces are plain stores (written through
+        // piecewise they would cost a memory write per piece), so the flag
+        // is a release store: one L2 write-back per tile.
+        __syncthreads();
+        if (tid == 0) publish_flag(p.ar_done + (m0 / C::BM) * p.tiles_n + tn, p.epoch);
       }
     }
   }
@@ -729,8 +738,13 @@ template <int BM, int NT>
 __device__ void build_row_perm(const GemmKParams& p, int* row_perm, int* row_key, int* scratch) {
   const int tid = threadIdx.x;
   const int tm = p.tiles_m;
-  if (p.perm_mode == kPermArrival) {
-    const int nflag = tm * (BM / kFlagRows);
+  if (p.perm_mode == kPermArrival || p.perm_mode == kPermPeerArrival) {
+    // Row tile i waits for flags: its own BM/128 flags (AllGather), or those
+    // of every peer for its rows (all-reduce: flag q * rbs + row block).
+    const int per = BM / kFlagRows;
+    const int npeer = p.perm_mode == kPermPeerArrival ? p.rs_npeers : 1;
+    const int rbs = tm * per;  // flags per peer
+    const int nflag = npeer * rbs;
     for (int i = tid; i < nflag; i += NT) {
       const int f = p.a_stage_order[i];
       if ((unsigned)f < (unsigned)nflag) scratch[f] = i;  // flag -> position
@@ -738,7 +752,8 @@ __device__ void build_row_perm(const GemmKParams& p, int* row_perm, int* row_key
     __syncthreads();
     for (int i = tid; i < tm; i += NT) {
       int key = 0;
-      for (int f = 0; f < BM / kFlagRows; ++f) key = max(key, scratch[i * (BM / kFlagRows) + f]);
+      for (int q = 0; q < npeer; ++q)
+        for (int f = 0; f < per; ++f) key = max(key, scratch[q * rbs + i * per + f]);
       scratch[nflag + i] = key;
     }
     __syncthreads();

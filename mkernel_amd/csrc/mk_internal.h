@@ -7,7 +7,7 @@
 namespace mk {
 
 enum Epilogue : int { kEpiStore = 0, kEpiSwiGLU = 1, kEpiReduce = 2 };
-enum PermMode : int { kPermNone = 0, kPermArrival = 1, kPermOwnedLast = 2 };
+enum PermMode : int { kPermNone = 0, kPermArrival = 1, kPermOwnedLast = 2, kPermPeerArrival = 3 };
 constexpr int kMaxTilesM = 512;
 constexpr int kMaxSplitListTiles = 4096;  // K-split with a permuted tile order: at most this many tiles
 constexpr int kMaxRounds = 64;   // cooperative staging between rounds: at most this many rounds
@@ -48,6 +48,7 @@ struct GemmKParams {
   const uint16_t* rs_recv;
   uint16_t* rs_out;
   const uint32_t* rs_flags;
+  uint32_t* ar_done;        // all-reduce: per output tile, epoch once its reduced bytes are visible
   // producer staging: block b (128 rows of st_cols) copied st_src -> st_dst
   const uint16_t* st_src;
   uint16_t* st_dst;

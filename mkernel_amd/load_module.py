@@ -10,6 +10,7 @@ name                           reference module definition
 =============================  ==============================================
 ``ag_gemm``                    include/operators/ag_gemm/session.cuh:192-230
 ``gemm_rs``                    include/operators/gemm_rs/session.cuh:103-154
+``gemm_ar``                    include/operators/gemm_ar/session.cuh:188-215
 ``dispatch_gemm``              include/operators/dispatch_gemm/session.cuh:89-133
 ``dispatch_gemm_glu_combine``  include/operators/dispatch_gemm_glu_combine/session.cuh:94-155
 =============================  ==============================================
@@ -211,6 +212,45 @@ def _rs_module():
                    commit_epoch=s.commit_epoch, zero_recv_buf=s.zero_recv_buf)
 
 
+# ---------------------------------------------------------------- gemm_ar ----
+def _ar_module():
+    s = _Session()
+
+    def gemm_ar_multinode(A, B, C, barrier, C_final, staging_buf_ptr, recv_buf_ptr, fifo_triggers, fifo_head,
+                          fifo_tail, fifo_tail_cache, fifo_capacity, arrival_flags_ptr, epoch, node_idx,
+                          num_intra_comm_sms, num_inter_comm_sms, ar_done_ptr, num_nodes=1, stage_order=None,
+                          **kwargs):
+        """GEMM + all-reduce (reference include/operators/gemm_ar/session.cuh:188-215,
+        src/gemm_ar.cu).
+
+        One GPU, world = ``C.local_world_size_``: ``C_final.data_`` [M, N] =
+        A @ B + the sum of the world-1 peer partials (fp32 adds, one bf16
+        rounding).  The partials to stage are at ``staging_buf_ptr``
+        [world-1, M, N] (device address; 0 = already in place); the
+        producer role copies them to ``recv_buf_ptr`` (same shape) and
+        publishes ``barrier`` words; each output tile is published in
+        ``ar_done_ptr`` (int32 [(M/256) * (N/256)], 0 = none) with the
+        epoch.  ``C`` is the rank's partial in the reference's multicast
+        buffer; on one GPU it is not written.  Remaining reference keyword
+        arguments (queues, tracing, RDMA) are accepted and ignored."""
+        Cf = _data(C_final)
+        M, N = A.shape[0], B.shape[1]
+        world = C.local_world_size_ if isinstance(C, DistBuffer) else 1
+        nflags = (world - 1) * M // 128
+        recv = _DevicePtr(int(recv_buf_ptr)) if world > 1 and recv_buf_ptr else None
+        if world > 1 and recv is None:
+            raise ValueError("recv_buf_ptr must point at the [world-1, M, N] receive buffer")
+        src = _DevicePtr(int(staging_buf_ptr)) if staging_buf_ptr else None
+        producers = (num_intra_comm_sms if num_intra_comm_sms > 0 else _DEFAULT_PRODUCERS) if src is not None else 0
+        fl = _flags(barrier, max(nflags, 1))
+        done = _DevicePtr(int(ar_done_ptr)) if ar_done_ptr else None
+        ops.gemm_ar(A, B, Cf, src, recv, world, fl, stage_order, epoch=int(epoch), gated=world > 1,
+                    num_producers=producers, stage_counters=_counters(fl), done_flags=done)
+        return Cf
+
+    return _module("gemm_ar", s, gemm_ar_multinode=gemm_ar_multinode, get_barrier_device_ptr=s.get_barrier_device_ptr)
+
+
 class _DevicePtr:
     """A raw device address passed where the C-ABI wants a pointer."""
 
@@ -292,6 +332,7 @@ def _glu_module():
 _BUILDERS = {
     "ag_gemm": _ag_module,
     "gemm_rs": _rs_module,
+    "gemm_ar": _ar_module,
     "dispatch_gemm": _dispatch_module,
     "dispatch_gemm_glu_combine": _glu_module,
 }

@@ -12,7 +12,7 @@ import numpy as np
 import torch
 
 from . import capi
-from .capi import (AgGemmArgs, GemmArgs, GemmRsArgs, MoeCombineArgs, MoeFfnArgs, MoeGroupedGemmArgs,
+from .capi import (AgGemmArgs, GemmArArgs, GemmArgs, GemmRsArgs, MoeCombineArgs, MoeFfnArgs, MoeGroupedGemmArgs,
                    MoeIndex, MoeIndexDevArgs, MoePermuteArgs)
 
 
@@ -104,6 +104,21 @@ def gemm_rs(A, B, workspace, output, peer_src, peer_recv, world: int, rank: int,
                       spin_limit, _ptr(error_word), _ptr(stage_counters), *_ws(split_ws, A.device))
     capi.call("mk_gemm_rs", args, _stream())
     return output
+
+
+def gemm_ar(A, B, C_final, peer_src, peer_recv, world: int, flags, stage_order, epoch: int, gated: bool = True,
+            num_producers: int = -1, num_cus: int = 0, spin_limit: int = 0, error_word=None, stage_counters=None,
+            done_flags=None, split_ws=None) -> torch.Tensor:
+    """GEMM + all-reduce at one rank's share (mk_gemm_ar): C_final = A @ B +
+    sum of the world-1 staged peer partials [world-1, M, N], fp32 adds."""
+    _bf16(A, "A"); _bf16(B, "B"); _bf16(C_final, "C_final")
+    M, K = A.shape
+    N = B.shape[1]
+    args = GemmArArgs(_ptr(A), _ptr(B), _ptr(C_final), _ptr(peer_src), _ptr(peer_recv), M, N, K, world, _ptr(flags),
+                      _ptr(stage_order), epoch, int(gated), num_producers, num_cus, spin_limit, _ptr(error_word),
+                      _ptr(stage_counters), _ptr(done_flags), *_ws(split_ws, A.device))
+    capi.call("mk_gemm_ar", args, _stream())
+    return C_final
 
 
 def moe_build_indices(topk_ids: np.ndarray, gates: np.ndarray, e0: int, n_local: int,

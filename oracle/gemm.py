@@ -47,6 +47,17 @@ def gemm_rs_ref(A: torch.Tensor, B: torch.Tensor, peer_partials: torch.Tensor, r
     return P, owned
 
 
+def gemm_ar_ref(A: torch.Tensor, B: torch.Tensor, peer_partials: torch.Tensor) -> torch.Tensor:
+    """All-reduce at one rank's share: A@B (fp32) + sum_p peer_partials[p]
+    (fp32, p ascending) over every row — the reference checks its C_final
+    against all_reduce(SUM) of the ranks' matmuls
+    (bench/gemm_ar_bench.py:510-514)."""
+    out = gemm_ref(A, B)
+    for p in range(peer_partials.shape[0]):
+        out += peer_partials[p].cpu().float()
+    return out
+
+
 def rel_fro(x: torch.Tensor, ref: torch.Tensor) -> float:
     """Relative Frobenius error ||x - ref||_F / ||ref||_F (float64)."""
     x = x.detach().cpu().double()

@@ -31,7 +31,7 @@ def test_library_exports_every_declared_symbol():
     assert L.mk_abi_version() == 2
 
 
-_STRUCTS = {"mk_gemm_args": capi.GemmArgs, "mk_ag_gemm_args": capi.AgGemmArgs, "mk_gemm_rs_args": capi.GemmRsArgs,
+_STRUCTS = {"mk_gemm_args": capi.GemmArgs, "mk_gemm_ar_args": capi.GemmArArgs, "mk_ag_gemm_args": capi.AgGemmArgs, "mk_gemm_rs_args": capi.GemmRsArgs,
             "mk_moe_index": capi.MoeIndex, "mk_moe_permute_args": capi.MoePermuteArgs,
             "mk_moe_grouped_gemm_args": capi.MoeGroupedGemmArgs, "mk_moe_combine_args": capi.MoeCombineArgs,
             "mk_moe_ffn_args": capi.MoeFfnArgs, "mk_moe_index_dev_args": capi.MoeIndexDevArgs}

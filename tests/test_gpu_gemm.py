@@ -259,3 +259,60 @@ def test_gemm_rs_equal_partials_known_answer(dev):
                 num_producers=0)
     torch.cuda.synchronize()
     assert torch.equal(out.cpu(), (own * world).to(torch.bfloat16))
+
+
+@pytest.mark.parametrize("producers,num_cus,M,N,K", [(-1, 0, 1024, 512, 256), (4, 0, 1024, 512, 256),
+                                                     (-1, 6, 2048, 768, 512), (0, 0, 512, 512, 128)])
+def test_gemm_ar_vs_oracle(dev, producers, num_cus, M, N, K):
+    """GEMM + all-reduce: C_final = A@B + sum of 7 staged peer partials over
+    all rows; staged bytes exact, every output tile published with the
+    epoch; arrival order of the peer blocks does not change a bit."""
+    _say(f"gemm_ar producers={producers} num_cus={num_cus} M={M} N={N} K={K}")
+    world = 8
+    A = wl.randn_bf16((M, K), 40, K ** -0.5)
+    B = wl.randn_bf16((K, N), 41, K ** -0.5)
+    peers = wl.randn_bf16((world - 1, M, N), 42, 0.5)
+    nflags = (world - 1) * M // 128
+    ntiles = (M // 256) * (N // 256)
+    ref = ag_ref = None
+    outs = []
+    for epoch, seed in [(3, 1), (4, 2)]:
+        order = torch.from_numpy(wl.stage_order(nflags, seed)).to(dev)
+        recv = torch.zeros((world - 1, M, N), dtype=torch.bfloat16, device=dev)
+        flags = torch.zeros(nflags, dtype=torch.int32, device=dev)
+        counters = torch.zeros_like(flags)
+        done = torch.zeros(ntiles, dtype=torch.int32, device=dev)
+        err = torch.zeros(1, dtype=torch.int32, device=dev)
+        C = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+        if producers == 0:  # partials already in place, flags published by someone else
+            recv.copy_(peers.to(dev))
+            flags.fill_(epoch)
+        ops.gemm_ar(A.to(dev), B.to(dev), C, peers.to(dev) if producers != 0 else None, recv, world, flags, order,
+                    epoch=epoch, num_producers=producers, num_cus=num_cus, stage_counters=counters, done_flags=done,
+                    spin_limit=4_000_000, error_word=err)
+        torch.cuda.synchronize()
+        assert int(err.item()) == 0, "a bounded wait timed out"
+        assert torch.equal(recv.cpu(), peers), "staged partials differ"
+        assert (done.cpu() == epoch).all(), "an output tile was not published"
+        outs.append(C.cpu())
+    from oracle.gemm import gemm_ar_ref
+    ref = gemm_ar_ref(A, B, peers)
+    assert rel_fro(outs[0].float(), ref) < TOL
+    assert torch.allclose(outs[0].float(), ref, rtol=2 ** -7, atol=1e-2)
+    assert torch.equal(outs[0], outs[1]), "result depends on the stage order"
+
+
+def test_gemm_ar_equal_partials_known_answer(dev):
+    """Every peer partial equal to the own partial => C_final is exactly 8x
+    it (integer operands, exact in fp32 and bf16)."""
+    M, K, N, world = 512, 128, 512, 8
+    g = torch.Generator().manual_seed(5)
+    A = torch.randint(-1, 2, (M, K), generator=g).to(torch.bfloat16)
+    B = torch.randint(-1, 2, (K, N), generator=g).to(torch.bfloat16)
+    P = A.float() @ B.float()
+    peers = P.to(torch.bfloat16).unsqueeze(0).repeat(world - 1, 1, 1).contiguous()
+    C = torch.zeros((M, N), dtype=torch.bfloat16, device=dev)
+    ops.gemm_ar(A.to(dev), B.to(dev), C, None, peers.to(dev), world, None, None, epoch=1, gated=False,
+                num_producers=0)
+    torch.cuda.synchronize()
+    assert torch.equal(C.cpu(), (P * world).to(torch.bfloat16))

@@ -173,3 +173,21 @@ def test_zipf_routing_properties():
     assert (np.diff(gates, axis=1) <= 1e-7).all()        # top-k in descending logit order
     ids2, gates2 = wl.zipf_routing(1000, 256, 8, 1.1, 6)
     assert np.array_equal(ids, ids2) and np.array_equal(gates, gates2)
+
+
+def test_gemm_ar_ref_known_answers():
+    """All-reduce: zero peers leave the plain GEMM; peers equal to the own
+    partial give exactly 8x it (integer operands: every sum is exact)."""
+    from oracle.gemm import gemm_ar_ref, gemm_ref
+    g = torch.Generator().manual_seed(2)
+    A = torch.randint(-2, 3, (64, 32), generator=g).to(torch.bfloat16)
+    B = torch.randint(-2, 3, (32, 48), generator=g).to(torch.bfloat16)
+    P = gemm_ref(A, B)
+    zero = torch.zeros((7, 64, 48), dtype=torch.bfloat16)
+    assert torch.equal(gemm_ar_ref(A, B, zero), P)
+    same = P.bfloat16()[None].expand(7, -1, -1)
+    assert torch.equal(gemm_ar_ref(A, B, same), 8 * P)
+    # brute force on a tiny case
+    a = torch.tensor([[1.0, 2.0]]).bfloat16(); b = torch.tensor([[3.0], [4.0]]).bfloat16()
+    peers = torch.tensor([[[0.5]], [[-2.0]]]).bfloat16()
+    assert gemm_ar_ref(a, b, peers).item() == 11.0 + 0.5 - 2.0

@@ -22,6 +22,10 @@ REF_ARGS = {
         "fifo_head", "fifo_tail", "fifo_tail_cache", "fifo_capacity", "arrival_flags_ptr", "epoch", "node_idx",
         "num_comp_sms", "num_intra_comm", "num_send_sms", "num_reduce_sms", "use_acquire_poll",
         "reduce_poll_sleep_ns", "ready_chunk", "staging", "num_nodes"],
+    ("gemm_ar", "gemm_ar_multinode"): [
+        "A", "B", "C", "barrier", "C_final", "staging_buf_ptr", "recv_buf_ptr", "fifo_triggers", "fifo_head",
+        "fifo_tail", "fifo_tail_cache", "fifo_capacity", "arrival_flags_ptr", "epoch", "node_idx",
+        "num_intra_comm_sms", "num_inter_comm_sms", "ar_done_ptr", "num_nodes"],
     ("dispatch_gemm", "moe_dispatch_gemm_fused"): [
         "pre_tokens", "peer_tokens", "copy_ready", "post_tokens", "weights", "outputs", "padded_tokens_per_expert",
         "pull_dispatch_indices", "local_rb_per_expert", "barrier", "sync_barrier", "recv_buf_ptr", "fifo_triggers",
@@ -136,3 +140,27 @@ def test_moe_reference_flows(dev):
     _, ye_ref = om.ffn_ref(post_ref, w1, w2, idx["padded_tokens_per_expert"], cfg.I)
     y_ref = om.combine_ref(ye_ref, idx["row_weight"], idx["pull_indices"], T)
     assert rel_fro(y_out.data_, y_ref) < 2e-2
+
+
+@pytest.mark.gpu
+def test_gemm_ar_reference_flow(dev):
+    """gemm_ar_multinode called the way the reference bench calls it
+    (bench/gemm_ar_bench.py:445-470): C_final = all-reduce of the partials."""
+    from oracle.gemm import gemm_ar_ref, rel_fro
+    mod = load_module.load("gemm_ar")
+    M, K, N, world = 1024, 256, 512, 8
+    A = wl.randn_bf16((M, K), 50, K ** -0.5)
+    B = wl.randn_bf16((K, N), 51, K ** -0.5)
+    peers = wl.randn_bf16((world - 1, M, N), 52, 0.5)
+    C = mod.DistBuffer((M, N), dtype=torch.bfloat16, local_rank=0, local_world_size=world)
+    C_final = mod.DistBuffer((M, N), dtype=torch.bfloat16, local_rank=0, local_world_size=world)
+    staging = peers.to(dev)
+    recv = torch.zeros_like(staging)
+    barrier = mod.DistBuffer(((world - 1) * M // 128,), dtype=torch.int32, local_rank=0, local_world_size=world)
+    ar_done = torch.zeros((M // 256) * (N // 256), dtype=torch.int32, device=dev)
+    mod.set_epoch(1)
+    mod.gemm_ar_multinode(A.to(dev), B.to(dev), C, barrier, C_final, staging.data_ptr(), recv.data_ptr(),
+                          0, 0, 0, 0, 0, 0, 1, 0, 4, 0, ar_done.data_ptr(), num_nodes=1)
+    torch.cuda.synchronize()
+    assert rel_fro(C_final.data_.float(), gemm_ar_ref(A, B, peers)) < 2e-2
+    assert (ar_done.cpu() == 1).all()
