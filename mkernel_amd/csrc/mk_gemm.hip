@@ -78,19 +78,26 @@ __device__ __forceinline__ void decode_grouped(int t, int tiles_m, int tiles_n, 
 }
 
 // Global column of B for LDS B-column q (q a multiple of 8).  With the SwiGLU
-// epilogue every wave's column range holds matching gate and up columns:
-// the first half of a wave's WTN columns are gate columns j, the second half
-// the up columns I + j.
+// epilogue a 256-column tile holds 128 gate columns (LDS columns 0..127:
+// gate columns tn*128 ..) and the 128 matching up columns (LDS 128..255:
+// I + tn*128 ..), so every B k-row is fetched as two 256-byte segments.
+// Wave wn's fragment jb reads 32-column LDS block jb*WN + wn (b_block), so
+// fragment jb and jb + FN/2 of one thread hold a gate and its up column.
 template <class C, int EPI>
 __device__ __forceinline__ int b_col(const GemmKParams& p, int tn, int q) {
   if constexpr (EPI == kEpiSwiGLU) {
-    constexpr int half = C::WTN / 2;
-    const int wn = q / C::WTN, r = q % C::WTN;
-    const int base = tn * (kBN / 2) + wn * half;
-    return r < half ? base + r : p.swiglu_I + base + (r - half);
+    constexpr int half = kBN / 2;
+    return q < half ? tn * half + q : p.swiglu_I + tn * half + (q - half);
   } else {
     return tn * kBN + q;
   }
+}
+
+// 32-column LDS block that wave wn's B fragment jb reads.
+template <class C, int EPI>
+__device__ __forceinline__ int b_block(int wn, int jb) {
+  if constexpr (EPI == kEpiSwiGLU) return jb * C::WN + wn;
+  else return wn * C::FN + jb;
 }
 
 // ---------------------------------------------------------------------------
@@ -185,7 +192,7 @@ __device__ __forceinline__ void store_tile(const GemmKParams& p, f32x16 (&acc)[C
 #pragma unroll
     for (int i = 0; i < C::FM; ++i) {
       const int m = m0 + wm * C::WTM + i * 32 + ml;
-      uint16_t* crow = p.C + (int64_t)m * p.ldc + tn * (kBN / 2) + wn * (C::WTN / 2) + 4 * kg;
+      uint16_t* crow = p.C + (int64_t)m * p.ldc + tn * (kBN / 2) + 4 * kg;
 #pragma unroll
       for (int j = 0; j < C::FN / 2; ++j)
 #pragma unroll
@@ -200,7 +207,7 @@ __device__ __forceinline__ void store_tile(const GemmKParams& p, f32x16 (&acc)[C
           uint2 w;
           w.x = pack_bf16x2(o[0], o[1]);
           w.y = pack_bf16x2(o[2], o[3]);
-          *reinterpret_cast<uint2*>(crow + j * 32 + 8 * a) = w;
+          *reinterpret_cast<uint2*>(crow + b_block<C, EPI>(wn, j) * 32 + 8 * a) = w;
         }
     }
   } else {  // kEpiReduce
@@ -451,7 +458,7 @@ __device__ void compute_role(const GemmKParams& p, int cons_id, char* smem, cons
 #pragma unroll
   for (int jb = 0; jb < C::FN; ++jb) {
     const int krow = 8 * (G >> 1) + jr;
-    const int c = 4 * (wn * C::FN + jb) + 2 * (G & 1) + (q >> 1);
+    const int c = 4 * b_block<C, EPI>(wn, jb) + 2 * (G & 1) + (q >> 1);
     b_rd[jb] = krow * 512 + ((c ^ (4 * (krow & 3))) << 4) + (q & 1) * 8;
   }
   const uint32_t lds_base = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)smem;
@@ -496,6 +503,7 @@ __device__ void compute_role(const GemmKParams& p, int cons_id, char* smem, cons
     // MFMAs of its 32-row blocks that hold padding only (their outputs stay
     // zero, as they would be from the zero-filled padding rows).
     int fm_active = C::FM;
+    const int rb_real = (C::BM == 128 && p.rb_rows) ? __builtin_amdgcn_readfirstlane(p.rb_rows[tm]) : C::BM;
     if (p.rb_rows) {
       const int real = __builtin_amdgcn_readfirstlane(p.rb_rows[tm]) - wm * C::WTM;
       fm_active = __builtin_amdgcn_readfirstlane(min(max((real + 31) / 32, 0), C::FM));
@@ -508,6 +516,8 @@ __device__ void compute_role(const GemmKParams& p, int cons_id, char* smem, cons
       __syncthreads();
     }
 
+    // Padding rows of a 128-row expert block (rb_rows) get an offset past the
+    // buffer's end too: the DMA returns zeros without touching memory.
     // Fused dispatch (grouped GEMMs with gather_pull): A rows are gathered
     // from the token buffer through the pull table — row r of the tile reads
     // token row (src_node * devs + src_dev) * tokens_per_src + src_token;
@@ -526,7 +536,10 @@ __device__ void compute_role(const GemmKParams& p, int cons_id, char* smem, cons
     for (int i = 0; i < C::A_INST; ++i) {
       const int row = (wave * C::A_INST + i) * 16 + (lane >> 2);
       const int c = (lane & 3) ^ ((row >> 2) & 3);
-      if (p.gather_pull) {
+      if (C::BM == 128 && p.rb_rows && row >= rb_real) {
+        // padding row of an expert block: read as zeros, no memory traffic
+        a_src[i] = 0x80000000u;
+      } else if (p.gather_pull) {
         const int* pr = p.gather_pull + 3 * (int64_t)(m0 + row);
         const int64_t srow = ((int64_t)pr[0] * p.gather_devs + pr[1]) * p.gather_tps + pr[2];
         a_src[i] = (pr[0] < 0 || pr[2] < 0) ? 0x80000000u : (uint32_t)(srow * p.lda * 2 + c * 16);
