@@ -84,16 +84,24 @@ constexpr int kPlanThreads = 1024;
 __global__ __launch_bounds__(kPlanThreads) void plan_kernel(IndexKParams p) {
   __shared__ int s[kPlanThreads];
   __shared__ int carry;
-  // per expert: totals, and the exclusive prefix over chunks (in place)
-  for (int e = threadIdx.x; e < p.n_local; e += kPlanThreads) {
+  // per expert: totals, and the exclusive prefix over chunks (in place);
+  // one wave per expert, 64 chunks per step, wave prefix sums by shuffles
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  for (int e = wave; e < p.n_local; e += kPlanThreads / 64) {
     int* h = p.hist + (int64_t)e * p.nchunks;
-    int run = 0;
-    for (int c = 0; c < p.nchunks; ++c) {
-      const int v = h[c];
-      h[c] = run;
-      run += v;
+    int carry_e = 0;
+    for (int c0 = 0; c0 < p.nchunks; c0 += 64) {
+      const int c = c0 + lane;
+      const int v = c < p.nchunks ? h[c] : 0;
+      int incl = v;
+      for (int d = 1; d < 64; d <<= 1) {
+        const int y = __shfl_up(incl, d, 64);
+        if (lane >= d) incl += y;
+      }
+      if (c < p.nchunks) h[c] = carry_e + incl - v;
+      carry_e += __shfl(incl, 63, 64);
     }
-    p.exp_cnt[e] = run;
+    if (lane == 0) p.exp_cnt[e] = carry_e;
   }
   __syncthreads();
   // padded expert offsets: exclusive scan over experts, kPlanThreads at a time
@@ -125,10 +133,10 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(IndexKParams p) {
   }
   __syncthreads();
   // chunk prefixes become absolute row bases
-  for (int e = threadIdx.x; e < p.n_local; e += kPlanThreads) {
+  for (int e = wave; e < p.n_local; e += kPlanThreads / 64) {
     int* h = p.hist + (int64_t)e * p.nchunks;
     const int off = p.exp_off[e];
-    for (int c = 0; c < p.nchunks; ++c) h[c] += off;
+    for (int c = lane; c < p.nchunks; c += 64) h[c] += off;
   }
 }
 
