@@ -196,20 +196,25 @@ def bench_moe(steps, warmup, extra):
                       "unfused": dispatch_gemm_unfused}, steps, warmup)
     ms4, ms4_unfused = r4["fused"], r4["unfused"]
     ms_perm = t.run(lambda i: ops.moe_permute(tokens, d["pull_indices"], post), steps, warmup)
-    ms_g1 = t.run(lambda i: ops.moe_grouped_gemm(post, w1, act, rb_expert=d["rb_expert"], mode=1,
-                                                 rb_rows=d["rb_rows"]), steps, warmup)
-    ms_g2 = t.run(lambda i: ops.moe_grouped_gemm(act, w2, ye, rb_expert=d["rb_expert"], mode=0,
-                                                 rb_rows=d["rb_rows"]), steps, warmup)
+    # the grouped GEMMs at the library's tile width and at 128 x 256
+    rg = interleaved({
+        "g1": lambda i: ops.moe_grouped_gemm(post, w1, act, rb_expert=d["rb_expert"], mode=1, rb_rows=d["rb_rows"]),
+        "g1_256": lambda i: ops.moe_grouped_gemm(post, w1, act, rb_expert=d["rb_expert"], mode=1,
+                                                 rb_rows=d["rb_rows"], tile_n=256),
+        "g2": lambda i: ops.moe_grouped_gemm(act, w2, ye, rb_expert=d["rb_expert"], mode=0, rb_rows=d["rb_rows"]),
+        "g2_256": lambda i: ops.moe_grouped_gemm(act, w2, ye, rb_expert=d["rb_expert"], mode=0,
+                                                 rb_rows=d["rb_rows"], tile_n=256)}, steps, warmup)
+    ms_g1, ms_g2 = rg["g1"], rg["g2"]
     ms_comb = t.run(lambda i: ops.moe_combine(ye, d["row_weight"], d["owner_offset"], d["slot_to_row"], y),
                     steps, warmup)
-    def ffn(fuse):
+    def ffn(fuse, tile_n=0):
         return lambda i: ops.moe_ffn_combine(tokens, d["pull_indices"], d["row_weight"], d["owner_offset"],
                                              d["slot_to_row"], w1, w2, post, act, ye, y, rb_expert=d["rb_expert"],
-                                             rb_rows=d["rb_rows"], fuse_dispatch=fuse)
+                                             rb_rows=d["rb_rows"], fuse_dispatch=fuse, tile_n=tile_n)
 
     # config 5: the layer with the dispatch fused into GEMM1 (the headline),
-    # and with the separate permute kernel
-    r5 = interleaved({"fused": ffn(True), "unfused": ffn(False)}, steps, warmup)
+    # with the separate permute kernel, and with 128 x 256 expert tiles
+    r5 = interleaved({"fused": ffn(True), "unfused": ffn(False), "fused_tile256": ffn(True, 256)}, steps, warmup)
     ms5, ms5_unfused = r5["fused"], r5["unfused"]
     # routing index build on the GPU (tables from device top-k ids / gates)
     ids_np, gates_np = wl.zipf_routing(cfg.tokens, cfg.experts, cfg.topk, cfg.zipf_s, 6)
@@ -232,6 +237,9 @@ def bench_moe(steps, warmup, extra):
                                    "permute_GBs": 2 * R_pad * cfg.H * 2 / ms_perm / 1e6}
     extra["moe_ffn_combine"] = {"us": ms5 * 1e3, "tokens_per_s": cfg.tokens / ms5 * 1e3, "tflops": f5 / ms5 / 1e9,
                                 "us_with_separate_permute": ms5_unfused * 1e3,
+                                "us_tile_128x256": r5["fused_tile256"] * 1e3,
+                                "us_gemm1_swiglu_tile_128x256": rg["g1_256"] * 1e3,
+                                "us_gemm2_tile_128x256": rg["g2_256"] * 1e3,
                                 "frac_peak": f5 / ms5 / 1e9 / PEAK_BF16_TFLOPS,
                                 "hbm_bound_GBs": layer_bytes / ms5 / 1e6,
                                 "us_gemm1_swiglu": ms_g1 * 1e3, "us_gemm2": ms_g2 * 1e3, "us_combine": ms_comb * 1e3,

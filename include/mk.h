@@ -276,6 +276,7 @@ typedef struct mk_moe_grouped_gemm_args {
   const int32_t* gather_pull;  /* [R_pad, 3] device, or NULL */
   int64_t n_src_rows;
   int32_t tokens_per_src, devs_per_node;
+  int32_t tile_n;              /* output tile width: 256, 512 (Nw % 512 == 0), or 0 = library choice */
 } mk_moe_grouped_gemm_args;
 int mk_moe_grouped_gemm(const mk_moe_grouped_gemm_args* args, void* stream);
 
@@ -333,6 +334,7 @@ typedef struct mk_moe_ffn_args {
   void* split_ws;              /* optional K-split workspace, as in mk_gemm_args */
   int64_t split_ws_bytes;
   int32_t fuse_dispatch;       /* 1: GEMM1 gathers tokens itself, post_tokens is not written */
+  int32_t tile_n;              /* grouped GEMM tile width, as in mk_moe_grouped_gemm_args */
 } mk_moe_ffn_args;
 int mk_moe_ffn_combine(const mk_moe_ffn_args* args, void* stream);
 

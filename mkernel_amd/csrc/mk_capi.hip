@@ -86,7 +86,7 @@ int check_gemm_shape(int64_t M, int64_t N, int64_t K, int bm) {
   return MK_OK;
 }
 
-constexpr int64_t kSplitTileBytes = 256 * 256 * 4;  // one fp32 BM x 256 partial (BM <= 256)
+constexpr int64_t kSplitTileBytes = 256 * 256 * 4;  // one fp32 partial tile (BM x BN <= 256 x 256)
 constexpr int64_t kSplitFlagBytes = 4096;           // flag words at the start of the workspace
 
 int64_t split_ws_bytes(int cus) { return kSplitFlagBytes + (int64_t)cus * kSplitTileBytes; }
@@ -96,7 +96,7 @@ int64_t split_ws_bytes(int cus) { return kSplitFlagBytes + (int64_t)cus * kSplit
 // K so that R*s workgroups share the round.  The workspace holds the flag
 // words at a fixed offset (so every plan finds them zeroed) followed by
 // R*(s-1) < n_cons <= CUs partial tiles, which split_ws_bytes covers.
-void plan_split(mk::GemmKParams& p, int bm, void* ws, int64_t ws_bytes) {
+void plan_split(mk::GemmKParams& p, int bm, void* ws, int64_t ws_bytes, int bn = 256) {
   const int ntiles = p.tiles_m * p.tiles_n;
   const int R = ntiles % p.n_cons;
   if (!ws || R == 0 || p.waves != 8) return;
@@ -105,7 +105,7 @@ void plan_split(mk::GemmKParams& p, int bm, void* ws, int64_t ws_bytes) {
   s = std::min(s, (p.K / 32) / 4);  // keep every part at >= 4 K stages
   if (s < 2) return;
   const int64_t parts = (int64_t)R * (s - 1);
-  if (parts * 4 > kSplitFlagBytes || kSplitFlagBytes + parts * bm * 256 * 4 > ws_bytes) return;
+  if (parts * 4 > kSplitFlagBytes || kSplitFlagBytes + parts * bm * bn * 4 > ws_bytes) return;
   p.sk_flags = static_cast<uint32_t*>(ws);
   p.sk_ws = reinterpret_cast<float*>(static_cast<char*>(ws) + kSplitFlagBytes);
   p.sk_full = ntiles - R;
@@ -130,7 +130,7 @@ extern "C" {
 
 const char* mk_last_error_string(void) { return g_err.c_str(); }
 
-int32_t mk_abi_version(void) { return 2; }
+int32_t mk_abi_version(void) { return 3; }
 
 int32_t mk_device_cu_count(void) {
   DevInfo d;
@@ -474,8 +474,11 @@ static int grouped_gemm_impl(const void* A, const void* W, void* out, const int3
                              const int32_t* expert_rows, const int32_t* rb_rows, int64_t R_pad, int64_t K,
                              int64_t Nw, int32_t E, int32_t mode, int32_t num_cus, void* split_ws,
                              int64_t split_ws_bytes, const int32_t* gather_pull, int64_t n_src_rows,
-                             int32_t tokens_per_src, int32_t devs_per_node, hipStream_t stream) {
+                             int32_t tokens_per_src, int32_t devs_per_node, int32_t tile_n, hipStream_t stream) {
   if (!A || !W || !out || (!rb_expert && !expert_rows)) return fail(MK_EINVAL, "mk_moe_grouped_gemm: null argument");
+  if (tile_n != 0 && tile_n != 256 && tile_n != 512)
+    return fail(MK_EINVAL, "mk_moe_grouped_gemm: tile_n must be 0, 256 or 512");
+  if (tile_n == 512 && Nw % 512) return fail(MK_ESHAPE, "mk_moe_grouped_gemm: tile_n 512 needs Nw %% 512 == 0");
   if (mode != 0 && mode != 1) return fail(MK_EINVAL, "mk_moe_grouped_gemm: mode must be 0 or 1");
   if (E <= 0) return fail(MK_EINVAL, "mk_moe_grouped_gemm: num_experts must be positive");
   if (R_pad == 0) return MK_OK;
@@ -494,8 +497,11 @@ static int grouped_gemm_impl(const void* A, const void* W, void* out, const int3
   p.lda = K; p.ldb = Nw; p.ldc = mode == 1 ? Nw / 2 : Nw;
   p.b_expert_stride = K * Nw;
   p.M = (int)R_pad; p.N = (int)Nw; p.K = (int)K;
+  // 128 x 512 tiles stream each expert's activation rows half as often per
+  // weight byte as 128 x 256 tiles.
+  const int bn = tile_n ? tile_n : (Nw % 512 == 0 ? 512 : 256);
   p.tiles_m = (int)(R_pad / 128);
-  p.tiles_n = (int)(Nw / 256);
+  p.tiles_n = (int)(Nw / bn);
   p.rb_expert = rb_expert;
   p.expert_rows = expert_rows;
   p.rb_rows = rb_rows;
@@ -508,8 +514,8 @@ static int grouped_gemm_impl(const void* A, const void* W, void* out, const int3
   const int total = num_cus > 0 ? num_cus : d.cus;
   set_grid(p, total, 0, p.tiles_m * p.tiles_n);
   if (int rc = check_ws(split_ws, split_ws_bytes, "mk_moe_grouped_gemm")) return rc;
-  plan_split(p, 128, split_ws, split_ws_bytes);
-  hipError_t e = mk::launch_gemm(p, 128, mode == 1 ? mk::kEpiSwiGLU : mk::kEpiStore, stream);
+  plan_split(p, 128, split_ws, split_ws_bytes, bn);
+  hipError_t e = mk::launch_gemm(p, 128, mode == 1 ? mk::kEpiSwiGLU : mk::kEpiStore, stream, bn);
   return e == hipSuccess ? MK_OK : hip_fail(e, "mk_moe_grouped_gemm launch");
 }
 
@@ -517,7 +523,7 @@ int mk_moe_grouped_gemm(const mk_moe_grouped_gemm_args* a, void* stream) {
   if (!a) return fail(MK_EINVAL, "mk_moe_grouped_gemm: null argument");
   return grouped_gemm_impl(a->A, a->W, a->out, a->rb_expert, a->padded_tokens_per_expert, a->rb_rows, a->R_pad, a->K, a->Nw, a->num_experts, a->mode,
                            a->num_cus, a->split_ws, a->split_ws_bytes, a->gather_pull, a->n_src_rows,
-                           a->tokens_per_src, a->devs_per_node, static_cast<hipStream_t>(stream));
+                           a->tokens_per_src, a->devs_per_node, a->tile_n, static_cast<hipStream_t>(stream));
 }
 
 int mk_moe_combine(const mk_moe_combine_args* a, void* stream) {
@@ -584,7 +590,7 @@ int mk_moe_ffn_combine(const mk_moe_ffn_args* a, void* stream) {
     if (int rc = grouped_gemm_impl(a->tokens, a->w1, a->act, a->rb_expert, a->padded_tokens_per_expert, a->rb_rows,
                                    a->R_pad, a->H, 2 * a->I, a->num_experts, 1, a->num_cus, a->split_ws,
                                    a->split_ws_bytes, a->pull_indices, a->n_src_rows, a->tokens_per_src,
-                                   a->devs_per_node, s))
+                                   a->devs_per_node, a->tile_n, s))
       return rc;
   } else {
     mk_moe_permute_args pa{a->tokens, a->pull_indices, a->post_tokens, a->R_pad, a->H,
@@ -592,12 +598,12 @@ int mk_moe_ffn_combine(const mk_moe_ffn_args* a, void* stream) {
     if (int rc = mk_moe_permute(&pa, stream)) return rc;
     if (int rc = grouped_gemm_impl(a->post_tokens, a->w1, a->act, a->rb_expert, a->padded_tokens_per_expert,
                                    a->rb_rows, a->R_pad, a->H, 2 * a->I, a->num_experts, 1, a->num_cus,
-                                   a->split_ws, a->split_ws_bytes, nullptr, 0, 0, 0, s))
+                                   a->split_ws, a->split_ws_bytes, nullptr, 0, 0, 0, a->tile_n, s))
       return rc;
   }
   if (int rc = grouped_gemm_impl(a->act, a->w2, a->y_expert, a->rb_expert, a->padded_tokens_per_expert,
                                  a->rb_rows, a->R_pad, a->I, a->H, a->num_experts, 0, a->num_cus, a->split_ws,
-                                 a->split_ws_bytes, nullptr, 0, 0, 0, s))
+                                 a->split_ws_bytes, nullptr, 0, 0, 0, a->tile_n, s))
     return rc;
   mk_moe_combine_args ca{a->y_expert, a->row_weight, a->owner_offset, a->slot_to_row, a->y_out,
                          a->num_tokens, a->H, a->out_dtype};

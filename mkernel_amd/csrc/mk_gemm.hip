@@ -4,7 +4,8 @@
 //     data (AllGather shards or peer partials) and release-store a flag per
 //     tile — the in-GPU stand-in for the reference's intra_comm_sm gather
 //     (reference src/ag_gemm.cu:31-215);
-//   * compute workgroups run BM x 256 output tiles on
+//   * compute workgroups run BM x BN output tiles (BN = 256; 512 for the
+//     128-row expert tiles of the grouped GEMMs) on
 //     v_mfma_f32_32x32x16_bf16, optionally acquire-waiting the A-row flags
 //     before a tile (reference src/ag_gemm.cu:374-377) and optionally folding
 //     staged peer partials into the epilogue (reference src/gemm_rs.cu:685-845
@@ -18,7 +19,7 @@
 //   A stage: BM rows x 64 B, K-contiguous; 16-byte unit c of row r lives at
 //            unit c ^ ((r >> 2) & 3), so MFMA operand reads (ds_read_b128,
 //            16 consecutive rows per 16-lane group) are bank-conflict free;
-//   B stage: 32 k-rows x 512 B, N-contiguous exactly as B is stored; unit c
+//   B stage: 32 k-rows x 2*BN B, N-contiguous exactly as B is stored; unit c
 //            of k-row k lives at c ^ (4 * (k & 3)).  MFMA B operands are read
 //            with ds_read_b64_tr_b16: inside each 16-lane group, lane 4j+q
 //            supplies 4 columns of k-row j and every lane receives one column
@@ -40,17 +41,20 @@ typedef uint32_t v2u32_t __attribute__((ext_vector_type(2)));
 // ---------------------------------------------------------------------------
 // Tile configuration
 // ---------------------------------------------------------------------------
-template <int BM_, int WAVES_>
+template <int BM_, int WAVES_, int BN_ = 256>
 struct Cfg {
-  static constexpr int BM = BM_, WAVES = WAVES_, NT = 64 * WAVES_;
+  static constexpr int BM = BM_, BN = BN_, WAVES = WAVES_, NT = 64 * WAVES_;
   static constexpr int WM = 2, WN = WAVES_ / 2;             // wave grid
-  static constexpr int WTM = BM / WM, WTN = kBN / WN;       // wave tile
+  static constexpr int WTM = BM / WM, WTN = BN / WN;        // wave tile
   static constexpr int FM = WTM / 32, FN = WTN / 32;        // 32x32 blocks per wave
   static constexpr int BKD = 32;                            // K per stage
   static constexpr uint32_t A_BYTES = BM * BKD * 2;         // BM x 64 B
-  static constexpr uint32_t B_BYTES = BKD * kBN * 2;        // 32 x 512 B
+  static constexpr uint32_t BROW = BN * 2;                  // bytes per LDS B k-row
+  static constexpr uint32_t B_BYTES = BKD * BROW;           // 32 k-rows
+  static constexpr int B_UPR = BN / 8;                      // 16-byte units per B k-row
   static constexpr uint32_t STAGE = A_BYTES + B_BYTES;
-  static constexpr int S = (BM == 256) ? 4 : 6;             // ring depth
+  // ring depth: as deep as the 160 KB LDS allows next to the static tables
+  static constexpr int S = (BN == 512) ? 3 : (BM == 256) ? 4 : 6;
   static constexpr uint32_t LDS_BYTES = S * STAGE;
   static constexpr int A_INST = A_BYTES / 1024 / WAVES_;    // DMA instructions per wave per stage
   static constexpr int B_INST = B_BYTES / 1024 / WAVES_;
@@ -86,10 +90,10 @@ __device__ __forceinline__ void decode_grouped(int t, int tiles_m, int tiles_n, 
 template <class C, int EPI>
 __device__ __forceinline__ int b_col(const GemmKParams& p, int tn, int q) {
   if constexpr (EPI == kEpiSwiGLU) {
-    constexpr int half = kBN / 2;
+    constexpr int half = C::BN / 2;
     return q < half ? tn * half + q : p.swiglu_I + tn * half + (q - half);
   } else {
-    return tn * kBN + q;
+    return tn * C::BN + q;
   }
 }
 
@@ -162,7 +166,7 @@ __device__ void coop_stage(const GemmKParams& p, int cid, int& q, int& batch, in
 }
 
 // ---------------------------------------------------------------------------
-// Epilogue of one BM x 256 tile.  acc[i][j][4a+b] is C[m][n] with
+// Epilogue of one BM x BN tile.  acc[i][j][4a+b] is C[m][n] with
 // m = m0 + wm*WTM + 32i + ml and n (in tile) = wn*WTN + 32j + 8a + 4kg + b.
 // ---------------------------------------------------------------------------
 template <class C, int EPI>
@@ -175,7 +179,7 @@ __device__ __forceinline__ void store_tile(const GemmKParams& p, f32x16 (&acc)[C
 #pragma unroll
     for (int i = 0; i < C::FM; ++i) {
       const int m = m0 + wm * C::WTM + i * 32 + ml;
-      uint16_t* crow = p.C + (int64_t)m * p.ldc + tn * kBN + wn * C::WTN + 4 * kg;
+      uint16_t* crow = p.C + (int64_t)m * p.ldc + tn * C::BN + wn * C::WTN + 4 * kg;
 #pragma unroll
       for (int j = 0; j < C::FN; ++j)
 #pragma unroll
@@ -192,7 +196,7 @@ __device__ __forceinline__ void store_tile(const GemmKParams& p, f32x16 (&acc)[C
 #pragma unroll
     for (int i = 0; i < C::FM; ++i) {
       const int m = m0 + wm * C::WTM + i * 32 + ml;
-      uint16_t* crow = p.C + (int64_t)m * p.ldc + tn * (kBN / 2) + 4 * kg;
+      uint16_t* crow = p.C + (int64_t)m * p.ldc + tn * (C::BN / 2) + 4 * kg;
 #pragma unroll
       for (int j = 0; j < C::FN / 2; ++j)
 #pragma unroll
@@ -216,7 +220,7 @@ __device__ __forceinline__ void store_tile(const GemmKParams& p, f32x16 (&acc)[C
 #pragma unroll
       for (int i = 0; i < C::FM; ++i) {
         const int m = m0 + wm * C::WTM + i * 32 + ml;
-        uint16_t* crow = p.C + (int64_t)m * p.ldc + tn * kBN + wn * C::WTN + 4 * kg;
+        uint16_t* crow = p.C + (int64_t)m * p.ldc + tn * C::BN + wn * C::WTN + 4 * kg;
 #pragma unroll
         for (int j = 0; j < C::FN; ++j)
 #pragma unroll
@@ -245,7 +249,7 @@ __device__ __forceinline__ void store_tile(const GemmKParams& p, f32x16 (&acc)[C
       uint32_t voff[C::FM];
 #pragma unroll
       for (int i = 0; i < C::FM; ++i)
-        voff[i] = (uint32_t)(((wm * C::WTM + i * 32 + ml) * p.ldc + tn * kBN + wn * C::WTN + 4 * kg) * 2);
+        voff[i] = (uint32_t)(((wm * C::WTM + i * 32 + ml) * p.ldc + tn * C::BN + wn * C::WTN + 4 * kg) * 2);
       for (int q = 0; q < p.rs_npeers; ++q) {
         const __amdgpu_buffer_rsrc_t r =
             make_rsrc(p.rs_recv + q * peer_stride + (int64_t)lr0 * p.ldc, (uint32_t)(C::BM * p.ldc * 2));
@@ -272,7 +276,7 @@ __device__ __forceinline__ void store_tile(const GemmKParams& p, f32x16 (&acc)[C
 #pragma unroll
       for (int i = 0; i < C::FM; ++i) {
         const int lr = lr0 + wm * C::WTM + i * 32 + ml;
-        uint16_t* orow = p.rs_out + (int64_t)lr * p.ldc + tn * kBN + wn * C::WTN + 4 * kg;
+        uint16_t* orow = p.rs_out + (int64_t)lr * p.ldc + tn * C::BN + wn * C::WTN + 4 * kg;
 #pragma unroll
         for (int j = 0; j < C::FN; ++j)
 #pragma unroll
@@ -388,7 +392,7 @@ struct StagePlan {
 // of the register file.
 template <class C>
 __device__ __forceinline__ void put_partial(float* dst, f32x16 (&acc)[C::FM][C::FN], int tid) {
-  const __amdgpu_buffer_rsrc_t r = make_rsrc(dst, (uint32_t)(C::BM * kBN * 4));
+  const __amdgpu_buffer_rsrc_t r = make_rsrc(dst, (uint32_t)(C::BM * C::BN * 4));
 #pragma unroll
   for (int i = 0; i < C::FM; ++i)
 #pragma unroll
@@ -405,7 +409,7 @@ __device__ __forceinline__ void put_partial(float* dst, f32x16 (&acc)[C::FM][C::
 
 template <class C>
 __device__ __forceinline__ void add_partial(const float* src, f32x16 (&acc)[C::FM][C::FN], int tid) {
-  const __amdgpu_buffer_rsrc_t r = make_rsrc(src, (uint32_t)(C::BM * kBN * 4));
+  const __amdgpu_buffer_rsrc_t r = make_rsrc(src, (uint32_t)(C::BM * C::BN * 4));
 #pragma unroll
   for (int i = 0; i < C::FM; ++i)
 #pragma unroll
@@ -459,7 +463,7 @@ __device__ void compute_role(const GemmKParams& p, int cons_id, char* smem, cons
   for (int jb = 0; jb < C::FN; ++jb) {
     const int krow = 8 * (G >> 1) + jr;
     const int c = 4 * b_block<C, EPI>(wn, jb) + 2 * (G & 1) + (q >> 1);
-    b_rd[jb] = krow * 512 + ((c ^ (4 * (krow & 3))) << 4) + (q & 1) * 8;
+    b_rd[jb] = krow * C::BROW + ((c ^ (4 * (krow & 3))) << 4) + (q & 1) * 8;
   }
   const uint32_t lds_base = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)smem;
   const uint32_t wave_u = __builtin_amdgcn_readfirstlane(wave);
@@ -528,9 +532,9 @@ __device__ void compute_role(const GemmKParams& p, int cons_id, char* smem, cons
                            : make_rsrc_v(p.A + (int64_t)m0 * p.lda, (uint32_t)(C::BM * p.lda * 2));
     const u32x4_t rB = make_rsrc_v(Bp, (uint32_t)(p.K * p.ldb * 2));
     // DMA source offsets: lane l of a wave instruction fills LDS unit l of a
-    // 1 KB block, i.e. (A) row 16*inst + l/4, unit l%4; (B) k-row 2*inst +
-    // l/32, unit l%32.  Each lane fetches the chunk whose swizzled home is
-    // that unit.
+    // 1 KB block, i.e. (A) row 16*inst + l/4, unit l%4; (B) k-row
+    // (64/B_UPR)*inst + l/B_UPR, unit l%B_UPR.  Each lane fetches the chunk
+    // whose swizzled home is that unit.
     uint32_t a_src[C::A_INST], b_src[C::B_INST];
 #pragma unroll
     for (int i = 0; i < C::A_INST; ++i) {
@@ -549,8 +553,8 @@ __device__ void compute_role(const GemmKParams& p, int cons_id, char* smem, cons
     }
 #pragma unroll
     for (int i = 0; i < C::B_INST; ++i) {
-      const int krow = (wave * C::B_INST + i) * 2 + (lane >> 5);
-      const int c = (lane & 31) ^ (4 * (krow & 3));
+      const int krow = (wave * C::B_INST + i) * (64 / C::B_UPR) + lane / C::B_UPR;
+      const int c = (lane % C::B_UPR) ^ (4 * (krow & 3));
       b_src[i] = (uint32_t)(krow * p.ldb * 2 + b_col<C, EPI>(p, tn, c * 8) * 2);
     }
     // Stage kt of this unit is global K stage k0 + kt, kept in ring slot kt % S.
@@ -579,8 +583,8 @@ __device__ void compute_role(const GemmKParams& p, int cons_id, char* smem, cons
       for (int i = 0; i < C::FM; ++i) af[kk][i] = *reinterpret_cast<const bf16x8*>(sA + a_rd[kk] + i * 32 * 64);
 #pragma unroll
       for (int j = 0; j < C::FN; ++j) {
-        const bf16x4_t lo = lds_tr4(sB + b_rd[j] + kk * 16 * 512);
-        const bf16x4_t hi = lds_tr4(sB + b_rd[j] + kk * 16 * 512 + 4 * 512);
+        const bf16x4_t lo = lds_tr4(sB + b_rd[j] + kk * 16 * C::BROW);
+        const bf16x4_t hi = lds_tr4(sB + b_rd[j] + kk * 16 * C::BROW + 4 * C::BROW);
         bfr[kk][j] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
       }
     };
@@ -719,7 +723,7 @@ __device__ void compute_role(const GemmKParams& p, int cons_id, char* smem, cons
   if (part > 0) {
     // K-split contributor: publish the partial for part 0 of this tile.
     const int slot = tail_idx * (p.sk_split - 1) + part - 1;
-    put_partial<C>(p.sk_ws + (int64_t)slot * (C::BM * kBN), acc, tid);
+    put_partial<C>(p.sk_ws + (int64_t)slot * (C::BM * C::BN), acc, tid);
     // write-through stores performed at agent scope, then a relaxed flag
     // (the protocol of copy_wt: no L2 write-back needed)
     wait_vmem_all();
@@ -735,7 +739,7 @@ __device__ void compute_role(const GemmKParams& p, int cons_id, char* smem, cons
       for (int q2 = 0; q2 < p.sk_split - 1; ++q2) wait_flag(p.sk_flags + slot0 + q2, 1u, p.spin_limit, p.err);
     __syncthreads();
     for (int q2 = 0; q2 < p.sk_split - 1; ++q2)
-      add_partial<C>(p.sk_ws + (int64_t)(slot0 + q2) * (C::BM * kBN), acc, tid);
+      add_partial<C>(p.sk_ws + (int64_t)(slot0 + q2) * (C::BM * C::BN), acc, tid);
     if (tid == 0)
       for (int q2 = 0; q2 < p.sk_split - 1; ++q2)
         __hip_atomic_store(p.sk_flags + slot0 + q2, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -853,9 +857,9 @@ __device__ void build_full_list(const GemmKParams& p, const int* row_perm, uint1
   __syncthreads();
 }
 
-template <int BM, int WAVES, int EPI>
+template <int BM, int WAVES, int EPI, int BN>
 __global__ __launch_bounds__(64 * WAVES, 1) void gemm_kernel(GemmKParams p) {
-  using C = Cfg<BM, WAVES>;
+  using C = Cfg<BM, WAVES, BN>;
   extern __shared__ __attribute__((aligned(16))) char smem[];
   __shared__ int row_perm[kMaxTilesM];
   __shared__ uint16_t full_list[kMaxSplitListTiles];
@@ -906,26 +910,37 @@ __global__ __launch_bounds__(64 * WAVES, 1) void gemm_kernel(GemmKParams p) {
 // ---------------------------------------------------------------------------
 // Host launchers
 // ---------------------------------------------------------------------------
-template <int BM, int WAVES, int EPI>
+template <int BM, int WAVES, int EPI, int BN>
 static hipError_t launch_t(const GemmKParams& p, hipStream_t stream) {
-  using C = Cfg<BM, WAVES>;
+  using C = Cfg<BM, WAVES, BN>;
   static bool attr_set = false;  // once per process (one attribute per kernel)
   if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_kernel<BM, WAVES, EPI>),
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_kernel<BM, WAVES, EPI, BN>),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, C::LDS_BYTES);
     if (e != hipSuccess) return e;
     attr_set = true;
   }
-  hipLaunchKernelGGL((gemm_kernel<BM, WAVES, EPI>), dim3(p.n_prod + p.n_cons), dim3(C::NT), C::LDS_BYTES, stream, p);
+  hipLaunchKernelGGL((gemm_kernel<BM, WAVES, EPI, BN>), dim3(p.n_prod + p.n_cons), dim3(C::NT), C::LDS_BYTES,
+                     stream, p);
   return hipGetLastError();
 }
 
 template <int BM, int EPI>
 static hipError_t launch_w(const GemmKParams& p, hipStream_t stream) {
-  return p.waves == 8 ? launch_t<BM, 8, EPI>(p, stream) : launch_t<BM, 4, EPI>(p, stream);
+  return p.waves == 8 ? launch_t<BM, 8, EPI, 256>(p, stream) : launch_t<BM, 4, EPI, 256>(p, stream);
 }
 
-hipError_t launch_gemm(const GemmKParams& p, int bm, int epi, hipStream_t stream) {
+// Tile BM x bn; bn = 512 exists for BM = 128 with the store and SwiGLU
+// epilogues (the grouped expert GEMMs: half the activation re-streaming per
+// weight byte of the 128 x 256 tile) and 8 waves.
+hipError_t launch_gemm(const GemmKParams& p, int bm, int epi, hipStream_t stream, int bn) {
+  if (bn == 512) {
+    if (bm != 128 || p.waves != 8) return hipErrorInvalidValue;
+    if (epi == kEpiStore) return launch_t<128, 8, kEpiStore, 512>(p, stream);
+    if (epi == kEpiSwiGLU) return launch_t<128, 8, kEpiSwiGLU, 512>(p, stream);
+    return hipErrorInvalidValue;
+  }
+  if (bn != 256) return hipErrorInvalidValue;
   if (bm == 256) {
     if (epi == kEpiStore) return launch_w<256, kEpiStore>(p, stream);
     if (epi == kEpiReduce) return launch_w<256, kEpiReduce>(p, stream);

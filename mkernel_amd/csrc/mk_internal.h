@@ -69,7 +69,7 @@ struct GemmKParams {
   uint32_t* err;
 };
 
-hipError_t launch_gemm(const GemmKParams& p, int bm, int epi, hipStream_t stream);
+hipError_t launch_gemm(const GemmKParams& p, int bm, int epi, hipStream_t stream, int bn = 256);
 
 struct PermuteKParams {
   const uint16_t* tokens;

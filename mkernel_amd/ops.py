@@ -215,8 +215,9 @@ def moe_permute(tokens, pull, post, tokens_per_src: int | None = None, devs_per_
 
 def moe_grouped_gemm(A, W, out, rb_expert=None, padded_tokens_per_expert=None, mode: int = 0, num_cus: int = 0,
                      rb_rows=None, split_ws=None, gather_pull=None, tokens_per_src: int | None = None,
-                     devs_per_node: int = 1):
-    """mode 0: out = A @ W[e]; mode 1: out = silu(h[:, :I]) * h[:, I:], h = A @ W[e]."""
+                     devs_per_node: int = 1, tile_n: int = 0):
+    """mode 0: out = A @ W[e]; mode 1: out = silu(h[:, :I]) * h[:, I:], h = A @ W[e].
+    tile_n: output tile width 256 or 512 (0: the library's choice)."""
     _bf16(A, "A"); _bf16(W, "W"); _bf16(out, "out")
     # with gather_pull, A is the token buffer and the rows come from the pull table
     R_pad = gather_pull.shape[0] if gather_pull is not None else A.shape[0]
@@ -225,7 +226,7 @@ def moe_grouped_gemm(A, W, out, rb_expert=None, padded_tokens_per_expert=None, m
     tps = A.shape[0] if tokens_per_src is None else tokens_per_src
     args = MoeGroupedGemmArgs(_ptr(A), _ptr(W), _ptr(out), _ptr(rb_expert), _ptr(padded_tokens_per_expert),
                               _ptr(rb_rows), R_pad, K, Nw, E, mode, num_cus, *_ws(split_ws, A.device),
-                              _ptr(gather_pull), A.shape[0], tps, devs_per_node)
+                              _ptr(gather_pull), A.shape[0], tps, devs_per_node, tile_n)
     capi.call("mk_moe_grouped_gemm", args, _stream())
     return out
 
@@ -257,7 +258,7 @@ def moe_combine(y_expert, row_weight, owner_offset, slot_to_row, y_out):
 def moe_ffn_combine(tokens, pull, row_weight, owner_offset, slot_to_row, w1, w2, post, act, y_expert, y_out,
                     rb_expert=None, padded_tokens_per_expert=None, tokens_per_src: int | None = None,
                     devs_per_node: int = 1, num_cus: int = 0, rb_rows=None, split_ws=None,
-                    fuse_dispatch: bool = False):
+                    fuse_dispatch: bool = False, tile_n: int = 0):
     """permute -> grouped GEMM1 + SwiGLU -> grouped GEMM2 -> combine.  With
     fuse_dispatch, GEMM1 reads the token rows through the pull table itself
     (no permute kernel, post may be None and is not written)."""
@@ -270,6 +271,6 @@ def moe_ffn_combine(tokens, pull, row_weight, owner_offset, slot_to_row, w1, w2,
                       _ptr(row_weight),
                       _ptr(owner_offset), _ptr(slot_to_row), _ptr(w1), _ptr(w2), _ptr(post), _ptr(act), _ptr(y_expert),
                       _ptr(y_out), T, tokens.shape[0], R_pad, H, I2 // 2, E, tps, devs_per_node, od, num_cus,
-                      *_ws(split_ws, tokens.device), int(fuse_dispatch))
+                      *_ws(split_ws, tokens.device), int(fuse_dispatch), tile_n)
     capi.call("mk_moe_ffn_combine", args, _stream())
     return y_out

@@ -34,18 +34,19 @@ def test_permute_bit_exact(dev):
     assert torch.equal(post.cpu(), om.permute_ref(tokens, idx["pull_indices"]))
 
 
+@pytest.mark.parametrize("tile_n", [256, 512])
 @pytest.mark.parametrize("split", [None, False])
 @pytest.mark.parametrize("use_rb,skip_pad", [(True, False), (False, False), (True, True)])
-def test_grouped_gemm1(dev, use_rb, skip_pad, split):
+def test_grouped_gemm1(dev, use_rb, skip_pad, split, tile_n):
     """split None: the tail round is K-split through the default workspace;
     False: no K-split."""
-    _say(f"moe grouped gemm1 use_rb={use_rb} skip_pad={skip_pad} split={split}")
+    _say(f"moe grouped gemm1 use_rb={use_rb} skip_pad={skip_pad} split={split} tile_n={tile_n}")
     tokens, ids, gates, w1, w2, idx, d = _setup(dev)
     post = om.permute_ref(tokens, idx["pull_indices"])
     out = torch.full((idx["R_pad"], 2 * SMALL.I), 3.0, dtype=torch.bfloat16, device=dev)
     ops.moe_grouped_gemm(post.to(dev), w1.to(dev), out, rb_expert=d["rb_expert"] if use_rb else None,
                          padded_tokens_per_expert=None if use_rb else d["padded_tokens_per_expert"], mode=0,
-                         rb_rows=d["rb_rows"] if skip_pad else None, split_ws=split)
+                         rb_rows=d["rb_rows"] if skip_pad else None, split_ws=split, tile_n=tile_n)
     torch.cuda.synchronize()
     ref = om.grouped_gemm_ref(post, w1, idx["padded_tokens_per_expert"])
     assert rel_fro(out.float(), ref) < TOL
@@ -53,16 +54,56 @@ def test_grouped_gemm1(dev, use_rb, skip_pad, split):
     assert (out.cpu()[torch.from_numpy(pad)] == 0).all()  # zero rows stay zero
 
 
+@pytest.mark.parametrize("tile_n", [256, 512])
 @pytest.mark.parametrize("split", [None, False])
-def test_gemm1_swiglu(dev, split):
-    _say(f"moe gemm1+swiglu split={split}")
+def test_gemm1_swiglu(dev, split, tile_n):
+    _say(f"moe gemm1+swiglu split={split} tile_n={tile_n}")
     tokens, ids, gates, w1, w2, idx, d = _setup(dev)
     post = om.permute_ref(tokens, idx["pull_indices"])
     act = torch.empty((idx["R_pad"], SMALL.I), dtype=torch.bfloat16, device=dev)
-    ops.moe_grouped_gemm(post.to(dev), w1.to(dev), act, rb_expert=d["rb_expert"], mode=1, split_ws=split)
+    ops.moe_grouped_gemm(post.to(dev), w1.to(dev), act, rb_expert=d["rb_expert"], mode=1, split_ws=split,
+                         tile_n=tile_n)
     torch.cuda.synchronize()
     ref_act, _ = om.ffn_ref(post, w1, w2, idx["padded_tokens_per_expert"], SMALL.I)
     assert rel_fro(act.float(), ref_act) < TOL
+
+
+WIDE = wl.MoeCfg(tokens=512, H=1024, I=512, experts=64, topk=8, ep=8, rank=1)
+
+
+@pytest.mark.parametrize("mode", [0, 1])
+def test_tile_widths_bit_identical(dev, mode):
+    """Without a K-split every output element is accumulated over the same K
+    stages in the same order by the 128x256 and the 128x512 tiles, so the two
+    widths give the same bits (pins the wide tile's B staging, SwiGLU column
+    pairing and store addressing against the narrow one)."""
+    _say(f"moe tile widths mode={mode}")
+    tokens, ids, gates, w1, w2, idx, d = _setup(dev, WIDE)
+    post = om.permute_ref(tokens, idx["pull_indices"]).to(dev)
+    ncol = 2 * WIDE.I if mode == 0 else WIDE.I
+    outs = []
+    for tn in (256, 512):
+        out = torch.full((idx["R_pad"], ncol), 5.0, dtype=torch.bfloat16, device=dev)
+        ops.moe_grouped_gemm(post, w1.to(dev), out, rb_expert=d["rb_expert"], mode=mode, rb_rows=d["rb_rows"],
+                             split_ws=False, tile_n=tn)
+        outs.append(out)
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0].cpu(), outs[1].cpu())
+    ref_act, _ = om.ffn_ref(post.cpu(), w1, w2, idx["padded_tokens_per_expert"], WIDE.I)
+    ref = ref_act if mode == 1 else om.grouped_gemm_ref(post.cpu(), w1, idx["padded_tokens_per_expert"])
+    assert rel_fro(outs[1].float(), ref) < TOL
+
+
+def test_grouped_gemm_tile_n_rejected(dev):
+    tokens, ids, gates, w1, w2, idx, d = _setup(dev)
+    post = om.permute_ref(tokens, idx["pull_indices"]).to(dev)
+    out = torch.empty((idx["R_pad"], SMALL.H), dtype=torch.bfloat16, device=dev)
+    w = torch.zeros((SMALL.n_local, SMALL.I, 768), dtype=torch.bfloat16, device=dev)
+    with pytest.raises(RuntimeError):
+        ops.moe_grouped_gemm(post[:, :SMALL.I].contiguous(), w, torch.empty((idx["R_pad"], 768), dtype=torch.bfloat16,
+                             device=dev), rb_expert=d["rb_expert"], tile_n=512)
+    with pytest.raises(RuntimeError):
+        ops.moe_grouped_gemm(post, w1.to(dev), out, rb_expert=d["rb_expert"], tile_n=384)
 
 
 def test_combine(dev):
@@ -94,8 +135,9 @@ def test_invert_slots_bit_exact(dev):
     assert np.array_equal(s2r.cpu().numpy(), idx["slot_to_row"])
 
 
-def test_ffn_combine_end_to_end(dev):
-    _say("moe ffn+combine")
+@pytest.mark.parametrize("tile_n", [0, 256])
+def test_ffn_combine_end_to_end(dev, tile_n):
+    _say(f"moe ffn+combine tile_n={tile_n}")
     tokens, ids, gates, w1, w2, idx, d = _setup(dev)
     R_pad = idx["R_pad"]
     post = torch.empty((R_pad, SMALL.H), dtype=torch.bfloat16, device=dev)
@@ -103,7 +145,8 @@ def test_ffn_combine_end_to_end(dev):
     ye = torch.empty((R_pad, SMALL.H), dtype=torch.bfloat16, device=dev)
     y = torch.empty((SMALL.tokens, SMALL.H), dtype=torch.bfloat16, device=dev)
     ops.moe_ffn_combine(tokens.to(dev), d["pull_indices"], d["row_weight"], d["owner_offset"], d["slot_to_row"],
-                        w1.to(dev), w2.to(dev), post, act, ye, y, rb_expert=d["rb_expert"], rb_rows=d["rb_rows"])
+                        w1.to(dev), w2.to(dev), post, act, ye, y, rb_expert=d["rb_expert"], rb_rows=d["rb_rows"],
+                        tile_n=tile_n)
     torch.cuda.synchronize()
     post_ref = om.permute_ref(tokens, idx["pull_indices"])
     assert torch.equal(post.cpu(), post_ref)
@@ -114,7 +157,7 @@ def test_ffn_combine_end_to_end(dev):
     # determinism: a second run is byte-identical
     y2 = torch.empty_like(y)
     ops.moe_ffn_combine(tokens.to(dev), d["pull_indices"], d["row_weight"], d["owner_offset"], d["slot_to_row"],
-                        w1.to(dev), w2.to(dev), post, act, ye, y2, rb_expert=d["rb_expert"])
+                        w1.to(dev), w2.to(dev), post, act, ye, y2, rb_expert=d["rb_expert"], tile_n=tile_n)
     torch.cuda.synchronize()
     assert torch.equal(y.cpu(), y2.cpu())
 
