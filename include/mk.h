@@ -284,6 +284,10 @@ int mk_moe_grouped_gemm(const mk_moe_grouped_gemm_args* args, void* stream);
  *   y[t] = sum_{s in [owner_offset[t], owner_offset[t+1])}
  *              row_weight[slot_to_row[s]] * y_expert[slot_to_row[s]]
  * products and sum in fp32; output fp32 (out_dtype 0) or bf16 (1).
+ * y_expert, row_weight and slot_to_row are read only inside owner_offset's
+ * ranges, so with no routed rows they may be NULL (then y = 0).  Every MoE
+ * entry accepts R_pad == 0 (no rows routed to this rank): permute and the
+ * grouped GEMMs do nothing and need no buffers.
  * Replaces combine_producer_fused + combine_gather_owner
  * (reference src/dispatch_gemm_glu_combine.cu:736-818). */
 typedef struct mk_moe_combine_args {

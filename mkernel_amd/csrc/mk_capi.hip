@@ -458,9 +458,11 @@ int mk_moe_build_indices(const int32_t* topk_ids, const float* gates, int32_t T,
 }
 
 int mk_moe_permute(const mk_moe_permute_args* a, void* stream) {
-  if (!a || !a->tokens || !a->pull_indices || !a->post_tokens) return fail(MK_EINVAL, "mk_moe_permute: null argument");
+  if (!a) return fail(MK_EINVAL, "mk_moe_permute: null argument");
   if (a->H <= 0 || a->H % 8) return fail(MK_ESHAPE, "mk_moe_permute: H must be a positive multiple of 8");
   if (a->R_pad < 0 || a->tokens_per_src <= 0 || a->devs_per_node <= 0) return fail(MK_EINVAL, "mk_moe_permute: bad sizes");
+  if (a->R_pad == 0) return MK_OK;  // no routed rows: nothing to copy
+  if (!a->tokens || !a->pull_indices || !a->post_tokens) return fail(MK_EINVAL, "mk_moe_permute: null argument");
   DevInfo d;
   if (int rc = device_info(&d)) return rc;
   mk::PermuteKParams p{static_cast<const uint16_t*>(a->tokens), a->pull_indices,
@@ -475,13 +477,14 @@ static int grouped_gemm_impl(const void* A, const void* W, void* out, const int3
                              int64_t Nw, int32_t E, int32_t mode, int32_t num_cus, void* split_ws,
                              int64_t split_ws_bytes, const int32_t* gather_pull, int64_t n_src_rows,
                              int32_t tokens_per_src, int32_t devs_per_node, int32_t tile_n, hipStream_t stream) {
-  if (!A || !W || !out || (!rb_expert && !expert_rows)) return fail(MK_EINVAL, "mk_moe_grouped_gemm: null argument");
   if (tile_n != 0 && tile_n != 256 && tile_n != 512)
     return fail(MK_EINVAL, "mk_moe_grouped_gemm: tile_n must be 0, 256 or 512");
   if (tile_n == 512 && Nw % 512) return fail(MK_ESHAPE, "mk_moe_grouped_gemm: tile_n 512 needs Nw %% 512 == 0");
   if (mode != 0 && mode != 1) return fail(MK_EINVAL, "mk_moe_grouped_gemm: mode must be 0 or 1");
   if (E <= 0) return fail(MK_EINVAL, "mk_moe_grouped_gemm: num_experts must be positive");
-  if (R_pad == 0) return MK_OK;
+  if (R_pad < 0) return fail(MK_ESHAPE, "mk_moe_grouped_gemm: R_pad < 0");
+  if (R_pad == 0) return MK_OK;  // no routed rows
+  if (!A || !W || !out || (!rb_expert && !expert_rows)) return fail(MK_EINVAL, "mk_moe_grouped_gemm: null argument");
   if (int rc = check_gemm_shape(R_pad, Nw, K, 128)) return rc;
   if (gather_pull && (n_src_rows <= 0 || tokens_per_src <= 0 || devs_per_node <= 0 ||
                       n_src_rows * K * 2 >= (1LL << 31)))
@@ -532,8 +535,11 @@ int mk_moe_grouped_gemm(const mk_moe_grouped_gemm_args* a, void* stream) {
 }
 
 int mk_moe_combine(const mk_moe_combine_args* a, void* stream) {
-  if (!a || !a->y_expert || !a->row_weight || !a->owner_offset || !a->y_out)
+  // y_expert, row_weight and slot_to_row are read only inside owner_offset's
+  // ranges: with no routed rows (every range empty) they may be NULL.
+  if (!a || !a->owner_offset || (!a->y_out && a->num_tokens > 0))
     return fail(MK_EINVAL, "mk_moe_combine: null argument");
+  if (a->num_tokens < 0) return fail(MK_ESHAPE, "mk_moe_combine: num_tokens < 0");
   if (a->H <= 0 || a->H % 8) return fail(MK_ESHAPE, "mk_moe_combine: H must be a positive multiple of 8");
   if (a->out_dtype != 0 && a->out_dtype != 1) return fail(MK_EINVAL, "mk_moe_combine: out_dtype must be 0 or 1");
   DevInfo d;
@@ -546,9 +552,9 @@ int mk_moe_combine(const mk_moe_combine_args* a, void* stream) {
 
 int mk_moe_invert_slots(const int32_t* row_to_slot, const int32_t* row_to_owner, int64_t R_pad,
                         int32_t* slot_to_row, void* stream) {
-  if (!row_to_slot || !row_to_owner || (!slot_to_row && R_pad > 0))
-    return fail(MK_EINVAL, "mk_moe_invert_slots: null argument");
   if (R_pad < 0) return fail(MK_EINVAL, "mk_moe_invert_slots: R_pad < 0");
+  if (R_pad == 0) return MK_OK;
+  if (!row_to_slot || !row_to_owner || !slot_to_row) return fail(MK_EINVAL, "mk_moe_invert_slots: null argument");
   DevInfo d;
   if (int rc = device_info(&d)) return rc;
   hipError_t e = mk::launch_invert_slots(row_to_slot, row_to_owner, R_pad, slot_to_row, static_cast<hipStream_t>(stream));
@@ -556,8 +562,9 @@ int mk_moe_invert_slots(const int32_t* row_to_slot, const int32_t* row_to_owner,
 }
 
 int mk_moe_tile_rows(const int32_t* pull_indices, int64_t R_pad, int32_t* rb_rows, void* stream) {
-  if (!pull_indices || (!rb_rows && R_pad > 0)) return fail(MK_EINVAL, "mk_moe_tile_rows: null argument");
   if (R_pad < 0 || R_pad % 128) return fail(MK_ESHAPE, "mk_moe_tile_rows: R_pad must be a multiple of 128");
+  if (R_pad == 0) return MK_OK;
+  if (!pull_indices || !rb_rows) return fail(MK_EINVAL, "mk_moe_tile_rows: null argument");
   DevInfo d;
   if (int rc = device_info(&d)) return rc;
   hipError_t e = mk::launch_tile_rows(pull_indices, R_pad, rb_rows, static_cast<hipStream_t>(stream));
@@ -591,7 +598,7 @@ int mk_moe_ffn_combine(const mk_moe_ffn_args* a, void* stream) {
   if (a->I % 128) return fail(MK_ESHAPE, "mk_moe_ffn_combine: I must be a multiple of 128");
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (a->fuse_dispatch) {
-    if (!a->pull_indices) return fail(MK_EINVAL, "mk_moe_ffn_combine: null argument");
+    if (!a->pull_indices && a->R_pad > 0) return fail(MK_EINVAL, "mk_moe_ffn_combine: null argument");
     if (int rc = grouped_gemm_impl(a->tokens, a->w1, a->act, a->rb_expert, a->padded_tokens_per_expert, a->rb_rows,
                                    a->R_pad, a->H, 2 * a->I, a->num_experts, 1, a->num_cus, a->split_ws,
                                    a->split_ws_bytes, a->pull_indices, a->n_src_rows, a->tokens_per_src,

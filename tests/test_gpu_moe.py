@@ -229,3 +229,61 @@ def test_ffn_combine_fused_dispatch_bit_identical(dev):
                             fuse_dispatch=fuse)
         ys.append(y.cpu())
     assert torch.equal(ys[0], ys[1])
+
+
+@pytest.mark.parametrize("fuse", [False, True])
+def test_ffn_combine_no_local_rows(dev, fuse):
+    """A rank that no token routes to: R_pad = 0, every table empty; the
+    layer writes y = 0 and launches no GEMM."""
+    _say(f"moe ffn no local rows fuse={fuse}")
+    cfg = wl.MoeCfg(tokens=64, H=512, I=256, experts=64, topk=4, ep=8, rank=1)
+    tokens, ids, gates, w1, w2 = wl.moe_inputs(cfg)
+    ids = np.where((ids >= cfg.e0) & (ids < cfg.e0 + cfg.n_local), 0, ids)  # expert 0 belongs to rank 0
+    idx = ops.moe_build_indices(ids, gates, cfg.e0, cfg.n_local)
+    assert idx["R"] == 0 and idx["R_pad"] == 0
+    d = {k: torch.from_numpy(np.ascontiguousarray(v)).to(dev) for k, v in idx.items() if isinstance(v, np.ndarray)}
+    empty = torch.empty((0, cfg.H), dtype=torch.bfloat16, device=dev)
+    act = torch.empty((0, cfg.I), dtype=torch.bfloat16, device=dev)
+    y = torch.full((cfg.tokens, cfg.H), 9.0, dtype=torch.float32, device=dev)
+    ops.moe_ffn_combine(tokens.to(dev), d["pull_indices"], d["row_weight"], d["owner_offset"], d["slot_to_row"],
+                        w1.to(dev), w2.to(dev), None if fuse else empty, act, empty, y, rb_expert=d["rb_expert"],
+                        rb_rows=d["rb_rows"], fuse_dispatch=fuse)
+    torch.cuda.synchronize()
+    assert (y.cpu() == 0).all()
+    # the single-stage entries accept the empty tables too
+    ops.moe_permute(tokens.to(dev), d["pull_indices"], empty)
+    ops.moe_grouped_gemm(empty, w1.to(dev), act, rb_expert=d["rb_expert"], mode=1)
+    ops.moe_tile_rows(d["pull_indices"], torch.empty((0,), dtype=torch.int32, device=dev))
+    ops.moe_invert_slots(d["row_to_slot"], d["row_to_owner"], torch.empty((0,), dtype=torch.int32, device=dev))
+    torch.cuda.synchronize()
+
+
+def test_ffn_combine_ragged_extremes(dev):
+    """One token sends all top-k choices to local experts (one of them
+    twice), most tokens send none: slots, padding and the combine handle
+    both ends."""
+    _say("moe ffn ragged extremes")
+    cfg = wl.MoeCfg(tokens=256, H=512, I=256, experts=64, topk=8, ep=8, rank=2)
+    tokens, ids, gates, w1, w2 = wl.moe_inputs(cfg)
+    local = (ids >= cfg.e0) & (ids < cfg.e0 + cfg.n_local)
+    ids = np.where(local, (ids + cfg.n_local) % cfg.experts, ids)  # route everything away...
+    ids[7] = cfg.e0 + np.array([0, 1, 2, 3, 4, 5, 6, 6])           # ...except token 7
+    ids[200, :2] = cfg.e0 + 3                                       # and two entries of token 200
+    idx = ops.moe_build_indices(ids, gates, cfg.e0, cfg.n_local)
+    assert idx["R"] == 10
+    d = {k: torch.from_numpy(np.ascontiguousarray(v)).to(dev) for k, v in idx.items() if isinstance(v, np.ndarray)}
+    R_pad = idx["R_pad"]
+    act = torch.empty((R_pad, cfg.I), dtype=torch.bfloat16, device=dev)
+    ye = torch.empty((R_pad, cfg.H), dtype=torch.bfloat16, device=dev)
+    y = torch.full((cfg.tokens, cfg.H), 9.0, dtype=torch.float32, device=dev)
+    ops.moe_ffn_combine(tokens.to(dev), d["pull_indices"], d["row_weight"], d["owner_offset"], d["slot_to_row"],
+                        w1.to(dev), w2.to(dev), None, act, ye, y, rb_expert=d["rb_expert"], rb_rows=d["rb_rows"],
+                        fuse_dispatch=True)
+    torch.cuda.synchronize()
+    post = om.permute_ref(tokens, idx["pull_indices"])
+    _, ye_ref = om.ffn_ref(post, w1, w2, idx["padded_tokens_per_expert"], cfg.I)
+    y_ref = om.combine_ref(ye_ref, idx["row_weight"], idx["pull_indices"], cfg.tokens)
+    assert rel_fro(y.float().cpu(), y_ref) < TOL
+    routed = torch.zeros(cfg.tokens, dtype=torch.bool)
+    routed[[7, 200]] = True
+    assert (y.cpu()[~routed] == 0).all()
