@@ -1,0 +1,132 @@
+"""GPU parity at the BASELINE configurations' full sizes.
+
+The CPU oracle cannot run a whole 16384-row GEMM in seconds, so each test
+checks sampled rows (or tokens) against the oracle and the rest through
+properties that hold at any size: staged bytes equal their source, every
+flag carries the epoch, a gated launch equals the ungated one bit for bit,
+and the output is finite everywhere."""
+import numpy as np
+import pytest
+import torch
+
+from mkernel_amd import ops, workloads as wl
+from oracle import moe as om
+from oracle.gemm import gemm_ref, rel_fro
+
+pytestmark = pytest.mark.gpu
+TOL = 2e-2
+
+
+def _say(msg):
+    print(msg, flush=True)
+
+
+def _sample_rows(n_rows: int, block: int, count: int, seed: int) -> np.ndarray:
+    """`count` whole 128-row blocks at seeded positions (sorted)."""
+    rng = np.random.default_rng(seed)
+    blocks = np.sort(rng.choice(n_rows // block, size=count, replace=False))
+    return np.concatenate([np.arange(b * block, (b + 1) * block) for b in blocks])
+
+
+def test_config2_ag_gemm_full(dev):
+    """Config 2: A_full 16384x8192 from 8 staged shards, B 8192x3584."""
+    _say("full config 2 ag_gemm")
+    cfg = wl.AgCfg()
+    A, B, order = wl.ag_inputs(cfg)
+    Ad, Bd = A.to(dev), B.to(dev)
+    A_full = torch.zeros_like(Ad)
+    flags = torch.zeros(cfg.M // 128, dtype=torch.int32, device=dev)
+    counters = torch.zeros_like(flags)
+    C = torch.empty((cfg.M, cfg.N), dtype=torch.bfloat16, device=dev)
+    err = torch.zeros(1, dtype=torch.int32, device=dev)
+    ops.ag_gemm(Ad, A_full, Bd, C, flags, torch.from_numpy(order).to(dev), epoch=3, stage_counters=counters,
+                spin_limit=1 << 26, error_word=err)
+    C_ungated = torch.empty_like(C)
+    ops.ag_gemm(None, A_full, Bd, C_ungated, None, None, epoch=1, gated=False, num_producers=0)
+    torch.cuda.synchronize()
+    assert int(err.item()) == 0
+    assert torch.equal(A_full, Ad)                       # every staged byte
+    assert (flags == 3).all()                            # every flag published at the epoch
+    assert torch.equal(C, C_ungated)                     # gating changes no output bit
+    assert torch.isfinite(C.float()).all()
+    rows = torch.from_numpy(_sample_rows(cfg.M, 128, 6, 11))
+    assert rel_fro(C.cpu()[rows].float(), gemm_ref(A[rows], B)) < TOL
+
+
+def test_config3_gemm_rs_full(dev):
+    """Config 3: A 16384x3584 @ B 3584x8192, 7 staged 2048x8192 peer partials
+    folded into rank 0's owned slice."""
+    _say("full config 3 gemm_rs")
+    cfg = wl.RsCfg()
+    A, B, peers, order = wl.rs_inputs(cfg)
+    rows = cfg.M // cfg.world
+    Ad, Bd, Pd = A.to(dev), B.to(dev), peers.to(dev)
+    work = torch.zeros((cfg.M, cfg.N), dtype=torch.bfloat16, device=dev)
+    out = torch.empty((rows, cfg.N), dtype=torch.bfloat16, device=dev)
+    recv = torch.zeros_like(Pd)
+    nfl = (cfg.world - 1) * rows // 128
+    flags = torch.zeros(nfl, dtype=torch.int32, device=dev)
+    counters = torch.zeros_like(flags)
+    err = torch.zeros(1, dtype=torch.int32, device=dev)
+    ops.gemm_rs(Ad, Bd, work, out, Pd, recv, cfg.world, cfg.rank, flags, torch.from_numpy(order).to(dev), epoch=5,
+                stage_counters=counters, spin_limit=1 << 26, error_word=err)
+    torch.cuda.synchronize()
+    assert int(err.item()) == 0
+    assert torch.equal(recv, Pd)
+    assert (flags == 5).all()
+    assert torch.isfinite(out.float()).all()
+    own0 = cfg.rank * rows
+    loc = torch.from_numpy(_sample_rows(rows, 128, 4, 12))
+    ref = gemm_ref(A[own0 + loc], B) + peers[:, loc].float().sum(0)
+    assert rel_fro(out.cpu()[loc].float(), ref) < TOL
+    # rows outside the owned slice hold the plain local partial
+    other = torch.from_numpy(_sample_rows(cfg.M - rows, 128, 3, 13)) + rows
+    assert rel_fro(work.cpu()[other].float(), gemm_ref(A[other], B)) < TOL
+    assert (work.cpu()[own0:own0 + rows] == 0).all()
+
+
+def test_config5_moe_layer_full(dev):
+    """Configs 4/5: 4096 tokens x 7168, top-8 of 256 (Zipf 1.1), 32 local
+    experts; the fused-dispatch layer checked on sampled tokens."""
+    _say("full config 5 moe layer")
+    cfg = wl.MoeCfg()
+    tokens, ids, gates, w1, w2 = wl.moe_inputs(cfg, device=dev)
+    idx = ops.moe_build_indices(ids, gates, cfg.e0, cfg.n_local)
+    d = {k: torch.from_numpy(np.ascontiguousarray(v)).to(dev) for k, v in idx.items() if isinstance(v, np.ndarray)}
+    R_pad = idx["R_pad"]
+    act = torch.empty((R_pad, cfg.I), dtype=torch.bfloat16, device=dev)
+    ye = torch.empty((R_pad, cfg.H), dtype=torch.bfloat16, device=dev)
+    y = torch.empty((cfg.tokens, cfg.H), dtype=torch.bfloat16, device=dev)
+    ops.moe_ffn_combine(tokens, d["pull_indices"], d["row_weight"], d["owner_offset"], d["slot_to_row"], w1, w2,
+                        None, act, ye, y, rb_expert=d["rb_expert"], rb_rows=d["rb_rows"], fuse_dispatch=True)
+    # config 4's unfused form (permute, then GEMM1) on the same tables
+    post = torch.empty((R_pad, cfg.H), dtype=torch.bfloat16, device=dev)
+    ops.moe_permute(tokens, d["pull_indices"], post)
+    torch.cuda.synchronize()
+    assert torch.isfinite(y.float()).all()
+    pull = idx["pull_indices"]
+    tok_cpu = tokens.cpu()
+    assert torch.equal(post.cpu(), om.permute_ref(tok_cpu, pull))   # permute bit-exact at full size
+    # sampled tokens: every routed row of each, through the oracle's FFN
+    rng = np.random.default_rng(14)
+    routed = np.unique(pull[pull[:, 0] >= 0, 2])
+    sample = np.sort(rng.choice(routed, size=24, replace=False))
+    offs = idx["owner_offset"]
+    y_ref = torch.zeros((len(sample), cfg.H))
+    by_expert = {}                                   # local expert -> [(sample index, row)]
+    for i, t in enumerate(sample):
+        for s in range(offs[t], offs[t + 1]):
+            r = int(idx["slot_to_row"][s])
+            by_expert.setdefault(int(idx["rb_expert"][r // 128]), []).append((i, r))
+    for e, items in by_expert.items():               # each expert's weights leave the GPU once
+        w1e, w2e = w1[e].cpu(), w2[e].cpu()
+        for i, r in items:
+            x = tok_cpu[int(pull[r, 2])][None]
+            h = gemm_ref(x, w1e)
+            a = om.silu_mul(h[:, :cfg.I], h[:, cfg.I:]).to(torch.bfloat16)   # act is stored in bf16
+            y_ref[i] += float(idx["row_weight"][r]) * gemm_ref(a, w2e)[0]
+    assert rel_fro(y.cpu()[torch.from_numpy(sample)].float(), y_ref) < TOL
+    # tokens with no local expert get exactly zero
+    unrouted = np.setdiff1d(np.arange(cfg.tokens), routed)
+    if len(unrouted):
+        assert (y.cpu()[torch.from_numpy(unrouted)] == 0).all()
