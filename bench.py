@@ -291,7 +291,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--producers", type=int, default=-1,
                     help="-1: cooperative staging by every workgroup; >0: dedicated producer workgroups")
-    ap.add_argument("--workload", default="all", choices=["all", "ag", "gemm", "rs", "ar", "moe", "calib"])
+    ap.add_argument("--workload", default="all", choices=["all", "ag", "gemm", "rs", "ar", "moe", "ceiling", "calib"])
     ap.add_argument("--no-cpu", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -338,6 +338,15 @@ def main():
     if args.workload in ("all", "moe"):
         log("[bench] moe configs 4/5")
         bench_moe(K, W, extra)
+    if args.workload in ("all", "ceiling"):
+        # What the matrix cores sustain on this board (power-limited clock),
+        # next to the published peak the roofline is priced against.
+        log("[bench] mfma ceiling probe")
+        c = ops.probe_mfma_ceiling()
+        c["frac_of_published_peak"] = c["tflops"] / PEAK_BF16_TFLOPS
+        if line is not None:
+            c["headline_frac_of_ceiling"] = line["value"] / c["tflops"]
+        extra["mfma_ceiling"] = c
     if args.workload == "calib":
         # HBM-counter calibration: libmk's permute kernel as a plain copy of
         # a known size (identity row map, 256 MiB read + 256 MiB written).

@@ -355,6 +355,18 @@ int mk_moe_ffn_combine(const mk_moe_ffn_args* args, void* stream);
  * simply idles (src/ag_gemm.cu:265-461). */
 int64_t mk_query_workspace_bytes(int32_t which, int64_t M, int64_t N, int64_t K);
 
+/* Diagnostic, no counterpart in the reference (its benches price against
+ * the published peak only): the MFMA throughput ceiling of the device under
+ * sustained load.  num_wg workgroups of mk_probe_threads() threads each run
+ * `iters` iterations of 16 independent v_mfma_f32_32x32x16_bf16 per wave
+ * (32768 FLOP each) on random bf16 operands, no memory traffic.
+ * sink: fp32 [num_wg * mk_probe_threads()] (keeps the work live);
+ * clocks: u64 [num_wg * 2] = per workgroup (shader clock cycles, 100 MHz
+ * constant-clock ticks) around the loop, whose ratio gives the engine clock
+ * the matrix cores ran at.  Used by bench.py next to the roofline. */
+int mk_probe_mfma_ceiling(int64_t iters, int32_t num_wg, float* sink, uint64_t* clocks, void* stream);
+int32_t mk_probe_threads(void);
+
 /* Number of compute units of the current device (0 if no device). */
 int32_t mk_device_cu_count(void);
 

@@ -14,7 +14,7 @@ PKG = Path(__file__).resolve().parent
 ROOT = PKG.parent
 CSRC = PKG / "csrc"
 LIB = PKG / "libmk.so"
-SOURCES = ["mk_gemm.hip", "mk_moe.hip", "mk_moe_index.hip", "mk_capi.hip"]
+SOURCES = ["mk_gemm.hip", "mk_moe.hip", "mk_moe_index.hip", "mk_probe.hip", "mk_capi.hip"]
 
 HIPCC_FLAGS = [
     "--offload-arch=gfx950",

@@ -30,6 +30,8 @@ EXPORTS = (
     "mk_moe_tile_rows",
     "mk_moe_ffn_combine",
     "mk_query_workspace_bytes",
+    "mk_probe_mfma_ceiling",
+    "mk_probe_threads",
     "mk_device_cu_count",
     "mk_last_error_string",
     "mk_abi_version",
@@ -147,6 +149,10 @@ def lib() -> C.CDLL:
         L.mk_moe_tile_rows.restype = C.c_int
         L.mk_query_workspace_bytes.argtypes = [i32, i64, i64, i64]
         L.mk_query_workspace_bytes.restype = i64
+        L.mk_probe_mfma_ceiling.argtypes = [i64, i32, vp, vp, vp]
+        L.mk_probe_mfma_ceiling.restype = C.c_int
+        L.mk_probe_threads.argtypes = []
+        L.mk_probe_threads.restype = i32
         L.mk_device_cu_count.argtypes = []
         L.mk_device_cu_count.restype = i32
         L.mk_last_error_string.argtypes = []

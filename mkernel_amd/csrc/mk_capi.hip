@@ -132,6 +132,17 @@ const char* mk_last_error_string(void) { return g_err.c_str(); }
 
 int32_t mk_abi_version(void) { return 3; }
 
+int mk_probe_mfma_ceiling(int64_t iters, int32_t num_wg, float* sink, uint64_t* clocks, void* stream) {
+  if (!sink || !clocks) return fail(MK_EINVAL, "mk_probe_mfma_ceiling: null argument");
+  if (iters <= 0 || num_wg <= 0) return fail(MK_EINVAL, "mk_probe_mfma_ceiling: iters and num_wg must be positive");
+  DevInfo d;
+  if (int rc = device_info(&d)) return rc;
+  hipError_t e = mk::launch_mfma_ceiling(iters, num_wg, 12345u, sink, clocks, static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? MK_OK : hip_fail(e, "mk_probe_mfma_ceiling launch");
+}
+
+int32_t mk_probe_threads(void) { return mk::probe_threads(); }
+
 int32_t mk_device_cu_count(void) {
   DevInfo d;
   if (device_info(&d) != MK_OK) return 0;

@@ -1,14 +1,14 @@
 // mk_device.h — device-side vocabulary shared by the libmk kernels (gfx950).
 //
 // * bf16 storage is uint16_t; MFMA operands are 8 x __bf16 vectors.
-// * LDS tiles hold 64-wide K slices, one 128-byte row per M (or N) index,
-//   with an XOR swizzle on 16-byte units (see lds_off).
-// * Flags are epoch-stamped 32-bit words: producers release-store the epoch,
-//   consumers poll with relaxed agent-scope atomic loads and acquire-fence
-//   once the epoch is seen.  This is the ordering contract of the reference's
-//   comm::atomic_u32 release_store_gpu / acquire_load_gpu pair
-//   (reference include/comm/atomic_u32.cuh:33-95) expressed with the HIP
-//   memory model.
+// * Flags are epoch-stamped 32-bit words.  Data is written through to agent
+//   scope (write-through stores, then s_waitcnt vmcnt(0)) and the flag is a
+//   relaxed agent-scope store; consumers poll with relaxed agent-scope loads
+//   and acquire-fence once the epoch is seen.  This is the ordering contract
+//   of the reference's comm::atomic_u32 release_store_gpu / acquire_load_gpu
+//   pair (reference include/comm/atomic_u32.cuh:33-95) expressed with the
+//   HIP memory model (publish_flag is the plain release store, for data
+//   written without write-through).
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -21,34 +21,12 @@ typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kThreads = 256;  // 4 wavefronts of 64
-constexpr int kBK = 64;        // K slice per pipeline stage
-constexpr int kBN = 256;       // N tile (LDS B tile rows)
+constexpr int kThreads = 256;  // 4 wavefronts of 64 (permute / combine kernels)
 constexpr int kFlagRows = 128; // flag granularity
-
-// Byte offset of 16-byte unit `c` (0..7, i.e. k = 8c..8c+7) of LDS row `n`.
-// Row pairs share one 256-byte line of the 64 LDS banks; the unit index is
-// XOR-swizzled with s(p) = ((p & 7) << 1) | ((p >> 3) & 1), p = n / 2, so that
-//   (a) 16 consecutive rows read at the same c        (MFMA operand reads),
-//   (b) rows 8*nc + i for 4 nc x 4 c, fixed i          (transposed B stores),
-//   (c) 2 rows x 8 units                               (A stores)
-// each touch 16 distinct 16-byte units (no bank conflicts for b128), and the
-// swizzle repeats every 32 rows, so rows n and n + 32*j differ by a constant.
-__device__ __forceinline__ uint32_t lds_off(uint32_t n, uint32_t c) {
-  const uint32_t p = n >> 1;
-  const uint32_t s = ((p & 7u) << 1) | ((p >> 3) & 1u);
-  return p * 256u + ((((c << 1) | (n & 1u)) ^ s) << 4);
-}
 
 // Buffer resource over `bytes` bytes at `base` (gfx9 descriptor word 3).
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
-}
-
-__device__ __forceinline__ uint4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
-  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-  u32x4 v = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, 0));
-  return make_uint4(v[0], v[1], v[2], v[3]);
 }
 
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {

@@ -92,6 +92,9 @@ struct CombineKParams {
 hipError_t launch_combine(const CombineKParams& p, hipStream_t stream);
 hipError_t launch_tile_rows(const int* pull, int64_t R_pad, int* rb_rows, hipStream_t stream);
 int64_t index_workspace_bytes(int T, int topk, int n_local);
+hipError_t launch_mfma_ceiling(int64_t iters, int n_wg, uint32_t seed, float* sink, uint64_t* clocks,
+                               hipStream_t stream);
+int probe_threads();
 hipError_t launch_invert_slots(const int* row_to_slot, const int* row_to_owner, int64_t R_pad, int* slot_to_row,
                                hipStream_t stream);
 

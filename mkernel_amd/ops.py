@@ -274,3 +274,31 @@ def moe_ffn_combine(tokens, pull, row_weight, owner_offset, slot_to_row, w1, w2,
                       *_ws(split_ws, tokens.device), int(fuse_dispatch), tile_n)
     capi.call("mk_moe_ffn_combine", args, _stream())
     return y_out
+
+
+def probe_mfma_ceiling(iters: int = 20000, num_wg: int = 0, reps: int = 3) -> dict:
+    """MFMA throughput ceiling of the current device under sustained load
+    (mk_probe_mfma_ceiling): one 8-wave workgroup per CU issuing independent
+    32x32x16 bf16 MFMAs on random operands, no memory traffic.  Returns the
+    median TFLOP/s over `reps` launches (HIP events on the launch stream) and
+    the engine clock those launches ran at (shader cycles / 100 MHz ticks)."""
+    L = capi.lib()
+    n_wg = num_wg or cu_count()
+    threads = int(L.mk_probe_threads())
+    sink = torch.empty(n_wg * threads, dtype=torch.float32, device="cuda")
+    clocks = torch.zeros(n_wg * 2, dtype=torch.int64, device="cuda")
+    flops = float(n_wg) * (threads // 64) * iters * 16 * 2 * 32 * 32 * 16
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    capi.check("mk_probe_mfma_ceiling", L.mk_probe_mfma_ceiling(iters // 10, n_wg, _ptr(sink), _ptr(clocks), _stream()))
+    res = []
+    for _ in range(reps):
+        s.record()
+        capi.check("mk_probe_mfma_ceiling", L.mk_probe_mfma_ceiling(iters, n_wg, _ptr(sink), _ptr(clocks), _stream()))
+        e.record()
+        torch.cuda.synchronize()
+        ck = clocks.view(n_wg, 2).cpu().double()
+        ghz = float((ck[:, 0] / ck[:, 1]).median()) * 0.1
+        res.append((s.elapsed_time(e), ghz))
+    ms, ghz = sorted(res)[len(res) // 2]
+    return {"tflops": flops / ms / 1e9, "sclk_ghz": ghz, "workgroups": n_wg, "us": ms * 1e3,
+            "finite": bool(torch.isfinite(sink).all())}

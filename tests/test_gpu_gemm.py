@@ -316,3 +316,15 @@ def test_gemm_ar_equal_partials_known_answer(dev):
                 num_producers=0)
     torch.cuda.synchronize()
     assert torch.equal(C.cpu(), (P * world).to(torch.bfloat16))
+
+
+def test_mfma_ceiling_probe(dev):
+    """The MFMA ceiling probe runs, keeps its work live and reports a clock in
+    the board's range; its throughput cannot exceed the published peak at the
+    clock it reports (4096 bf16 FLOP per clock per CU)."""
+    _say("mfma ceiling probe")
+    r = ops.probe_mfma_ceiling(iters=2000, reps=1)
+    assert r["finite"]
+    assert 0.3 < r["sclk_ghz"] < 3.0
+    bound = ops.cu_count() * 4096 * r["sclk_ghz"] * 1e9 / 1e12
+    assert 0 < r["tflops"] <= bound * 1.05
