@@ -658,30 +658,112 @@ __device__ void compute_role(const GemmKParams& p, int cons_id, char* smem, cons
       // Every wave's last LDS read happened before the loop's final barrier,
       // so the ring is free for the next unit's prologue.
     } else {
-      // Lockstep schedule (one wave per SIMD).  Steady state for stage kt:
-      //   read kk=1 operands | MFMA kk=0 | wait stage kt+1 + barrier |
-      //   refill the slot with stage kt+S | read stage kt+1 kk=0 | MFMA kk=1
-      // so the barrier and the LDS reads overlap MFMAs already issued.  The
-      // last stage is peeled off: with no branch around the barrier block
-      // the compiler's LDS wait counts stay exact.
+      // Interleaved schedule (one wave per SIMD, S stages in flight).  Each
+      // stage kt is two half-steps of NM MFMAs:
+      //   A: MFMAs of sub-step 0 | reads of sub-step 1 (same stage)
+      //   wait for stage kt+1, barrier
+      //   B: MFMAs of sub-step 1 | refill of stage kt's slot with stage
+      //      kt+S, then reads of stage kt+1 sub-step 0
+      // and every LDS read and DMA instruction is pinned between two MFMAs:
+      // one wave per SIMD has no partner wave to cover its issue slots, so
+      // anything issued in a row with nothing in the matrix pipe is lost
+      // MFMA time.  Issue is in order, so an instruction placed after an
+      // MFMA goes out while that MFMA occupies the pipe.
+      constexpr int NM = C::FM * C::FN;      // MFMAs per K sub-step
+      constexpr int NR = C::FM + 2 * C::FN;  // LDS reads per K sub-step
+      constexpr int NPA = C::A_INST / 2, NP = NPA + C::B_INST / 2;  // DMA pairs per stage
+      static_assert(C::A_INST % 2 == 0 && C::B_INST % 2 == 0 && 2 * NP <= NM, "4-wave schedule shape");
+      bf16x4_t blo[2][C::FN], bhi[2][C::FN];
+      // read r of sub-step kk of ring slot `slot`: A fragments first, then
+      // the two transposing halves of each B fragment
+      auto rd = [&](int slot, int kk, int r) {
+        const char* sA = smem + slot * C::STAGE;
+        const char* sB = sA + C::A_BYTES;
+        if (r < C::FM) {
+          af[kk][r] = *reinterpret_cast<const bf16x8*>(sA + a_rd[kk] + r * 32 * 64);
+        } else {
+          const int j = (r - C::FM) >> 1;
+          if (((r - C::FM) & 1) == 0) blo[kk][j] = lds_tr4(sB + b_rd[j] + kk * 16 * C::BROW);
+          else bhi[kk][j] = lds_tr4(sB + b_rd[j] + kk * 16 * C::BROW + 4 * C::BROW);
+        }
+      };
+      auto mm = [&](int kk, int x) {
+        const int i = x / C::FN, j = x % C::FN;
+        if (C::BM == 128 && i >= fm_active) return;  // padding-only 32-row block of an expert tile
+        const bf16x8 bv = __builtin_shufflevector(blo[kk][j], bhi[kk][j], 0, 1, 2, 3, 4, 5, 6, 7);
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bv, af[kk][i], acc[i][j], 0, 0, 0);
+      };
+      // NM MFMAs of sub-step kk starting at x0, with reads (rslot, rkk)
+      // r = 0..NR-1 spread evenly behind them
+      auto mfma_reads = [&](int kk, int x0, int rslot, int rkk) {
+        constexpr int n = NM;  // upper bound of the loop below; x0 > 0 shortens it
+#pragma unroll
+        for (int x = 0; x < n; ++x) {
+          if (x < x0) continue;
+          mm(kk, x);
+          const int r0 = (x - x0) * NR / (NM - x0), r1 = (x - x0 + 1) * NR / (NM - x0);
+#pragma unroll
+          for (int r = r0; r < r1; ++r) rd(rslot, rkk, r);
+        }
+#pragma unroll
+        for (int x = 0; x < n; ++x) {
+          if (x < x0) continue;
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+          const int r0 = (x - x0) * NR / (NM - x0), r1 = (x - x0 + 1) * NR / (NM - x0);
+#pragma unroll
+          for (int r = r0; r < r1; ++r) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // its LDS reads
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      };
+      // half-step B with the refill of slot kt % S by stage kt + S: the DMA
+      // pairs ride behind the first 2*NP MFMAs (inline asm, pinned by
+      // sched_barrier), the reads of stage kt+1 behind the rest
+      auto half_b_refill = [&](int kt) {
+        const uint32_t st = lds_base + (uint32_t)(kt % C::S) * C::STAGE;
+        const uint32_t ka = (uint32_t)(k0 + kt + C::S) * (C::BKD * 2);
+        const uint32_t kb = (uint32_t)(k0 + kt + C::S) * (C::BKD * p.ldb * 2);
+#pragma unroll
+        for (int q = 0; q < NP; ++q) {
+          mm(1, 2 * q);
+          mm(1, 2 * q + 1);
+          __builtin_amdgcn_sched_barrier(0);
+          if (q < NPA) {
+            const uint32_t l = st + wave_u * C::A_INST * 1024 + 2 * q * 1024;
+            dma16x2(rA, l, l + 1024, a_src[2 * q], a_src[2 * q + 1], ka);
+          } else {
+            const int qb = q - NPA;
+            const uint32_t l = st + C::A_BYTES + wave_u * C::B_INST * 1024 + 2 * qb * 1024;
+            dma16x2(rB, l, l + 1024, b_src[2 * qb], b_src[2 * qb + 1], kb);
+          }
+          __builtin_amdgcn_sched_barrier(0);
+        }
+        mfma_reads(1, 2 * NP, (kt + 1) % C::S, 0);
+      };
 #pragma unroll
       for (int s = 0; s < C::S; ++s)
         if (s < nk) issue(s);
       wait_stage<C::S + 1, C::LOADS>(min(C::S - 1, nk - 1));
       __syncthreads();
-      read_frags(0, 0);
-      for (int kt = 0; kt < nk - 1; ++kt) {
-        read_frags(kt % C::S, 1);
-        mfma(0);
-        wait_stage<C::S + 1, C::LOADS>(min(C::S - 1, nk - 1 - kt) - 1);
+#pragma unroll
+      for (int r = 0; r < NR; ++r) rd(0, 0, r);
+      int kt = 0;
+      // steady state: every iteration refills the slot it finished
+      for (; kt + C::S < nk; ++kt) {
+        mfma_reads(0, 0, kt % C::S, 1);
+        wait_vm<(C::S - 2) * C::LOADS>();  // stage kt+1 landed (S-2 younger stages in flight)
         __syncthreads();
-        if (kt + C::S < nk) issue(kt + C::S);
-        read_frags((kt + 1) % C::S, 0);
-        mfma(1);
+        half_b_refill(kt);
       }
-      read_frags((nk - 1) % C::S, 1);
-      mfma(0);
-      mfma(1);
+      // drain: every stage is issued
+      for (; kt < nk - 1; ++kt) {
+        mfma_reads(0, 0, kt % C::S, 1);
+        wait_stage<C::S + 1, C::LOADS>(nk - 2 - kt);
+        __syncthreads();
+        mfma_reads(1, 0, (kt + 1) % C::S, 0);
+      }
+      mfma_reads(0, 0, (nk - 1) % C::S, 1);
+#pragma unroll
+      for (int x = 0; x < NM; ++x) mm(1, x);
       // Every wave must be done with the ring before the next unit's DMA.
       __syncthreads();
     }
