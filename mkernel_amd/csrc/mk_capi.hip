@@ -76,13 +76,22 @@ void set_grid(mk::GemmKParams& p, int total, int n_prod, int ntiles) {
   p.xcd_remap = (p.n_cons % 8 == 0 && p.n_prod % 8 == 0) ? 1 : 0;
 }
 
-int check_gemm_shape(int64_t M, int64_t N, int64_t K, int bm) {
+int check_gemm_shape(int64_t M, int64_t N, int64_t K, int bm, int64_t lda = 0, int64_t ldb = 0) {
   if (M <= 0 || N <= 0 || K <= 0) return fail(MK_ESHAPE, "M, N, K must be positive (got %lld, %lld, %lld)",
                                               (long long)M, (long long)N, (long long)K);
   if (M % bm) return fail(MK_ESHAPE, "M=%lld must be a multiple of %d", (long long)M, bm);
   if (N % 256) return fail(MK_ESHAPE, "N=%lld must be a multiple of 256", (long long)N);
   if (K % 32) return fail(MK_ESHAPE, "K=%lld must be a multiple of 32", (long long)K);
   if (M > (1LL << 30) || N > (1LL << 30) || K > (1LL << 30)) return fail(MK_ESHAPE, "dimension too large");
+  // The K loop addresses operands through buffer descriptors with 32-bit
+  // offsets: one row tile of A (whose padding rows use offsets from 2^31
+  // up, past the window) and all of B (one expert's B for grouped GEMMs).
+  if (lda <= 0) lda = K;
+  if (ldb <= 0) ldb = N;
+  if ((int64_t)bm * lda * 2 >= (1LL << 31))
+    return fail(MK_ESHAPE, "a %d-row tile of A (lda=%lld) must span less than 2 GiB", bm, (long long)lda);
+  if (K * ldb * 2 >= (1LL << 32))
+    return fail(MK_ESHAPE, "B (K=%lld x ldb=%lld) must be smaller than 4 GiB", (long long)K, (long long)ldb);
   return MK_OK;
 }
 
@@ -167,7 +176,7 @@ int mk_gemm(const mk_gemm_args* a, void* stream) {
   }
   if (bm != 128 && bm != 256) return fail(MK_EINVAL, "mk_gemm: tile_m must be 0, 128 or 256");
   if (a->waves != 0 && a->waves != 4 && a->waves != 8) return fail(MK_EINVAL, "mk_gemm: waves must be 0, 4 or 8");
-  if (int rc = check_gemm_shape(a->M, a->N, a->K, bm)) return rc;
+  if (int rc = check_gemm_shape(a->M, a->N, a->K, bm, a->lda, a->ldb)) return rc;
   if (a->lda < a->K || a->ldb < a->N || a->ldc < a->N || (a->lda | a->ldb | a->ldc) % 8)
     return fail(MK_ESHAPE, "mk_gemm: leading dimensions must cover the row and be multiples of 8");
   if (!aligned16(a->A) || !aligned16(a->B) || !aligned16(a->C))

@@ -1,5 +1,7 @@
 """GPU parity of the GEMM core, the flag-gated AllGather consumer and the
 reduce-scatter epilogue against the CPU oracle (all through the C-ABI)."""
+import ctypes as C
+
 import numpy as np
 import pytest
 import torch
@@ -328,3 +330,15 @@ def test_mfma_ceiling_probe(dev):
     assert 0.3 < r["sclk_ghz"] < 3.0
     bound = ops.cu_count() * 4096 * r["sclk_ghz"] * 1e9 / 1e12
     assert 0 < r["tflops"] <= bound * 1.05
+
+
+@pytest.mark.parametrize("M,N,K,lda", [(256, 32768, 65536, 65536), (256, 256, 32, 1 << 22)])
+def test_gemm_rejects_operands_beyond_32bit_windows(dev, M, N, K, lda):
+    """B of 4 GiB or more, or a 256-row A tile spanning 2 GiB, is beyond the
+    kernel's 32-bit buffer offsets: the call fails with a shape error before
+    touching memory (the pointers here are a small real buffer)."""
+    from mkernel_amd import capi
+    buf = torch.zeros(1024, dtype=torch.bfloat16, device=dev)
+    a = capi.GemmArgs(buf.data_ptr(), buf.data_ptr(), buf.data_ptr(), M, N, K, lda, N, N, 0, 256, 0, None, 0)
+    rc = capi.lib().mk_gemm(C.byref(a), None)
+    assert rc == -2, capi.lib().mk_last_error_string()
