@@ -39,26 +39,39 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
 __device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 
-// Wait until *flag has reached `epoch` (wrap-safe).  Polls are relaxed
-// agent-scope loads spaced by s_sleep with a growing interval (64 .. 1024
-// cycles), so a few hundred waiting workgroups do not flood the L2 the
-// producers are writing through; one acquire fence follows the successful
-// poll.  Returns false (and sets bit 0 of *err) after `limit` polls when
-// limit != 0.
-__device__ __forceinline__ bool wait_flag(const uint32_t* flag, uint32_t epoch, uint32_t limit,
-                                          uint32_t* err) {
-  uint32_t polls = 0;
-  while (true) {
-    const uint32_t v = __hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if ((int32_t)(v - epoch) >= 0) break;
-    if (limit != 0 && ++polls >= limit) {
-      if (err) __hip_atomic_fetch_or(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      return false;
+// Wait until every flag addr(0) .. addr(n-1) has reached `epoch`
+// (wrap-safe).  Each round loads all flags still pending at once (relaxed
+// agent-scope loads issued back to back: one memory latency per round, not
+// per flag), in chunks of kChunk (<= 32); rounds are spaced by s_sleep with a growing
+// interval (64 .. 1024 cycles), so a few hundred waiting workgroups do not
+// flood the L2 the producers are writing through.  One acquire fence
+// follows.  Returns false (and sets bit 0 of *err) after `limit` rounds of
+// one chunk when limit != 0.
+template <int kChunk, class Addr>
+__device__ __forceinline__ bool wait_flags(Addr addr, int n, uint32_t epoch, uint32_t limit, uint32_t* err) {
+  static_assert(kChunk >= 1 && kChunk <= 32, "flag chunk");
+  for (int base = 0; base < n; base += kChunk) {
+    const int m = min(n - base, kChunk);
+    uint32_t pending = m == 32 ? ~0u : (1u << m) - 1u;
+    uint32_t polls = 0;
+    while (true) {
+      uint32_t v[kChunk];
+#pragma unroll
+      for (int f = 0; f < kChunk; ++f)
+        if ((pending >> f) & 1u) v[f] = __hip_atomic_load(addr(base + f), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+      for (int f = 0; f < kChunk; ++f)
+        if (((pending >> f) & 1u) && (int32_t)(v[f] - epoch) >= 0) pending &= ~(1u << f);
+      if (!pending) break;
+      if (limit != 0 && ++polls >= limit) {
+        if (err) __hip_atomic_fetch_or(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return false;
+      }
+      if (polls < 8) __builtin_amdgcn_s_sleep(1);
+      else if (polls < 64) __builtin_amdgcn_s_sleep(4);
+      else __builtin_amdgcn_s_sleep(16);
+      if (limit == 0) ++polls;
     }
-    if (polls < 8) __builtin_amdgcn_s_sleep(1);
-    else if (polls < 64) __builtin_amdgcn_s_sleep(4);
-    else __builtin_amdgcn_s_sleep(16);
-    if (limit == 0) ++polls;
   }
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
   return true;

@@ -237,8 +237,8 @@ __device__ __forceinline__ void store_tile(const GemmKParams& p, f32x16 (&acc)[C
         const int rbs = p.rs_own_rows / kFlagRows;
         constexpr int per = C::BM / kFlagRows;
         if (tid == 0)
-          for (int f = 0; f < p.rs_npeers * per; ++f)
-            wait_flag(p.rs_flags + (f / per) * rbs + lr0 / kFlagRows + f % per, p.epoch, p.spin_limit, p.err);
+          wait_flags<16>([&](int f) { return p.rs_flags + (f / per) * rbs + lr0 / kFlagRows + f % per; },
+                     p.rs_npeers * per, p.epoch, p.spin_limit, p.err);
         __syncthreads();
       }
       // Fold the peers' bf16 partials into the fp32 accumulators, peer by
@@ -516,7 +516,8 @@ __device__ void compute_role(const GemmKParams& p, int cons_id, char* smem, cons
     // Flag gate on the A rows of this tile (AllGather consumer side).
     if (p.a_flags) {
       if (tid == 0)
-        for (int f = 0; f < C::BM / kFlagRows; ++f) wait_flag(p.a_flags + m0 / kFlagRows + f, p.epoch, p.spin_limit, p.err);
+        wait_flags<C::BM / kFlagRows>([&](int f) { return p.a_flags + m0 / kFlagRows + f; }, C::BM / kFlagRows, p.epoch, p.spin_limit,
+                   p.err);
       __syncthreads();
     }
 
@@ -818,7 +819,9 @@ __device__ void compute_role(const GemmKParams& p, int cons_id, char* smem, cons
     // order, and clear the flags for the next launch on this workspace.
     const int slot0 = tail_idx * (p.sk_split - 1);
     if (tid == 0)
-      for (int q2 = 0; q2 < p.sk_split - 1; ++q2) wait_flag(p.sk_flags + slot0 + q2, 1u, p.spin_limit, p.err);
+      // one flag at a time: the split unit's registers are at the limit
+      for (int q2 = 0; q2 < p.sk_split - 1; ++q2)
+        wait_flags<1>([&](int) { return p.sk_flags + slot0 + q2; }, 1, 1u, p.spin_limit, p.err);
     __syncthreads();
     for (int q2 = 0; q2 < p.sk_split - 1; ++q2)
       add_partial<C>(p.sk_ws + (int64_t)(slot0 + q2) * (C::BM * C::BN), acc, tid);
