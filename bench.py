@@ -89,6 +89,8 @@ def bench_ag(steps, warmup, producers, extra):
     flags_pub = torch.full_like(flags, 2 ** 30)
     r = interleaved({
         "gated": lambda i: gated(i, producers),
+        # cooperative staging with every workgroup copying before every round
+        "even_share": lambda i: gated(i, -2),
         "dedicated": lambda i: gated(i, 32),
         "ungated": lambda i: ops.ag_gemm(None, A_full, B, C, None, None, epoch=1, gated=False, num_producers=0),
         # gated, flags already published (pure gating cost, all CUs computing)
@@ -104,6 +106,7 @@ def bench_ag(steps, warmup, producers, extra):
         "us_gated_producer": ms * 1e3, "us_gated_producer_interleaved_median": ms_med * 1e3,
         "us_ungated": ms_ungated * 1e3, "us_gated_flags_preset": ms_preset * 1e3,
         "us_gated_32_dedicated_producers": ms_dedicated * 1e3,
+        "us_gated_even_share_staging": r["even_share"] * 1e3,
         "tflops_gated_producer": flops / ms / 1e9, "tflops_ungated": flops / ms_ungated / 1e9,
         "gating_overhead_producer": ms_med / ms_ungated - 1.0,
         "gating_overhead_flag_check": ms_preset / ms_ungated - 1.0,
@@ -290,7 +293,8 @@ def main():
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--producers", type=int, default=-1,
-                    help="-1: cooperative staging by every workgroup; >0: dedicated producer workgroups")
+                    help="-1: cooperative staging, halves of the grid alternating; -2: cooperative, every "
+                         "workgroup before every round; >0: dedicated producer workgroups")
     ap.add_argument("--workload", default="all", choices=["all", "ag", "gemm", "rs", "ar", "moe", "ceiling", "calib"])
     ap.add_argument("--no-cpu", action="store_true")
     args = ap.parse_args()

@@ -70,11 +70,17 @@ int mk_gemm(const mk_gemm_args* args, void* stream);
  *   gated, producers == 0  : flags are published by someone else
  *   gated, producers  > 0  : that many producer workgroups run inside the
  *                            launch beside the compute workgroups
- *   gated, producers == -1 : cooperative staging — every workgroup first
- *                            copies its share of 128 KB pieces (in stage
- *                            order), counting pieces per tile in
+ *   gated, producers == -1 : cooperative staging — the compute workgroups
+ *                            copy 128 KB pieces (in stage order) between
+ *                            their tile rounds, counting pieces per tile in
  *                            stage_counters; the workgroup that completes a
- *                            tile publishes its flag; then all compute    */
+ *                            tile publishes its flag.  Before round 0 every
+ *                            workgroup copies what round 0 waits for; after
+ *                            that the two halves of the grid (XCDs 0-3 and
+ *                            4-7) take turns: one copies ahead for the next
+ *                            round while the other computes
+ *   gated, producers == -2 : cooperative staging with every workgroup
+ *                            copying an even share before every round    */
 typedef struct mk_ag_gemm_args {
   const void* A_shards;  /* bf16 [M, K]: shards stacked in rank order (source) */
   void* A_full;          /* bf16 [M, K]: gathered A (destination / GEMM input) */
@@ -121,7 +127,7 @@ typedef struct mk_gemm_rs_args {
   const int32_t* stage_order;   /* [(world-1) * (M/world)/128]; NULL = ascending */
   uint32_t epoch;
   int32_t gated;
-  int32_t num_producers;        /* as in mk_ag_gemm (-1 = cooperative staging) */
+  int32_t num_producers;        /* as in mk_ag_gemm; -1 and -2 = cooperative staging, even share */
   int32_t num_cus;
   uint32_t spin_limit;
   uint32_t* error_word;
@@ -160,7 +166,7 @@ typedef struct mk_gemm_ar_args {
   const int32_t* stage_order;   /* [(world-1) * M/128]; NULL = ascending, no arrival order */
   uint32_t epoch;
   int32_t gated;
-  int32_t num_producers;        /* as in mk_ag_gemm (-1 = cooperative staging) */
+  int32_t num_producers;        /* as in mk_ag_gemm; -1 and -2 = cooperative staging, even share */
   int32_t num_cus;
   uint32_t spin_limit;
   uint32_t* error_word;

@@ -122,15 +122,16 @@ __device__ void producer_role(const GemmKParams& p, int pid) {
 
 // Cooperative staging: every compute workgroup copies its share of the
 // staging pieces (kPieces per 128-row block; global piece q is piece
-// q % kPieces of the block at stage position q / kPieces, and workgroup c
-// owns pieces c, c + n_cons, ...).  Each finished piece bumps its block's
+// q % kPieces of the block at stage position q / kPieces; a workgroup
+// copies pieces q, q + stride, ... — stride n_cons when every workgroup
+// shares a range, the group size when one half of the grid does).  Each finished piece bumps its block's
 // counter; the workgroup whose increment completes the block publishes the
 // block's flag.  Counters are never reset: completion is detected modulo
 // kPieces.  A workgroup stages in increasing q and may stop at any limit and
 // resume later (q and batch are its cursor), which lets the copy run between
 // tile rounds instead of all before the first one.
 template <int NT>
-__device__ void coop_stage(const GemmKParams& p, int cid, int& q, int& batch, int limit) {
+__device__ void coop_stage(const GemmKParams& p, int stride, int& q, int& batch, int limit) {
   const int64_t block_elems = (int64_t)kFlagRows * p.st_cols;
   const int64_t piece_vec = block_elems / 8 / kPieces;  // 16-byte units per piece
   limit = min(limit, p.st_nblocks * kPieces);
@@ -156,7 +157,7 @@ __device__ void coop_stage(const GemmKParams& p, int cid, int& q, int& batch, in
   while (q < limit) {
     int bs[8];
     int n = 0;
-    for (; n < batch && q < limit; ++n, q += p.n_cons) bs[n] = copy_piece(q);
+    for (; n < batch && q < limit; ++n, q += stride) bs[n] = copy_piece(q);
     wait_vmem_all();
     __syncthreads();
     if (threadIdx.x == 0)
@@ -379,8 +380,57 @@ __device__ __forceinline__ bf16x4_t lds_tr4(const char* p) {
 struct StagePlan {
   const int* round_need;  // per round: last stage position it waits for (null: staged up front)
   int n_rounds;
-  int q, batch;           // coop_stage cursor
+  int q, batch;           // coop_stage cursor (even-share mode)
+  int grp, gid, gsize;    // alternating mode: half of the grid (0/1), id in it, its size (0: even share)
 };
+
+// Piece count that rounds 0..r need staged (r = n_rounds: every piece).
+__device__ __forceinline__ int need_pieces(const GemmKParams& p, const StagePlan& sp, int r) {
+  const int total = p.st_nblocks * kPieces;
+  if (r >= sp.n_rounds) return total;
+  int need = 0;
+  for (int i = 0; i <= r; ++i) need = max(need, (sp.round_need[i] + 1) * kPieces);
+  return min(need, total);
+}
+
+// Alternating cooperative staging, before whole-tile round w.  Window w
+// (before round w) brings the staged pieces up to target(w): at least what
+// round w+1 waits for and at least an even share (target(-1): what round 0
+// waits for, copied by every workgroup before round 0).  Window w is
+// copied by one half of the grid, w % 2, while the other half computes;
+// the last window by every workgroup.  128 CUs already saturate HBM with a
+// copy, so a half moves a window's pieces about as fast as the whole grid
+// would, and each workgroup spends about half as long copying as when every
+// workgroup copies before every round.  The halves are XCDs 0-3 and 4-7
+// (consumer ids are XCD-major), so tiles sharing an XCD's L2 stay in step.
+template <int NT>
+__device__ void alt_stage(const GemmKParams& p, int cons_id, StagePlan& sp, int w) {
+  const int total = p.st_nblocks * kPieces;
+  const int n = sp.n_rounds;
+  // Even part of the target: windows 0..n-2 alternate halves (half 0 has
+  // h0 = ceil((n-1)/2) of them, half 1 h1 = floor); each half's windows
+  // carry equal shares of its half of the pieces left after round 0's, so
+  // both halves copy the same amount when the waits do not force more into
+  // early windows.
+  const int h0 = n / 2, h1 = (n - 1) / 2;
+  auto target = [&](int win) {
+    if (win < 0) return need_pieces(p, sp, 0);
+    if (win >= n - 1) return total;
+    const int c0 = win / 2 + 1, c1 = (win + 1) / 2;  // windows 0..win of each half
+    const int base = need_pieces(p, sp, 0), rest = total - base;  // pieces after the first window
+    const int64_t even = h1 > 0 ? base + ((int64_t)rest * c0 * h1 + (int64_t)rest * c1 * h0) / (2LL * h0 * h1)
+                                : (int64_t)total;
+    return max(need_pieces(p, sp, win + 1), (int)min<int64_t>(even, total));
+  };
+  auto copy_range = [&](int lo, int hi, int id, int stride) {
+    int q = lo + id, batch = 1;
+    coop_stage<NT>(p, stride, q, batch, hi);
+  };
+  if (w == 0) copy_range(0, target(-1), cons_id, p.n_cons);
+  const int lo = target(w - 1), hi = max(lo, target(w));
+  if (w == n - 1) copy_range(lo, hi, cons_id, p.n_cons);
+  else if (w % 2 == sp.grp) copy_range(lo, hi, sp.gid, sp.gsize);
+}
 
 // Partial-sum exchange for K-split tail tiles.  A tile's NT threads hold
 // FM*FN*16 fp32 accumulators each; they go to the workspace as 16-byte
@@ -779,12 +829,14 @@ __device__ void compute_role(const GemmKParams& p, int cons_id, char* smem, cons
   // the arrival order.
   const int st_total = p.st_nblocks * kPieces;
   for (int w = 0; w < n_full_mine; ++w) {
-    if (sp.round_need) {
+    if (sp.round_need && sp.gsize > 0 && w < sp.n_rounds) {
+      alt_stage<C::NT>(p, cons_id, sp, w);
+    } else if (sp.round_need) {
       // this tile is in round w: stage what round w waits for, and at least
       // an even share of the rest
       const int need = (sp.round_need[w] + 1) * kPieces;
       const int even = (int)((int64_t)st_total * (w + 1) / sp.n_rounds);
-      coop_stage<C::NT>(p, cons_id, sp.q, sp.batch, max(need, even));
+      coop_stage<C::NT>(p, p.n_cons, sp.q, sp.batch, max(need, even));
     }
     int t = cons_id + w * p.n_cons;
     if (full_list) t = full_list[t];
@@ -793,7 +845,11 @@ __device__ void compute_role(const GemmKParams& p, int cons_id, char* smem, cons
     tile_body(t, row_perm != nullptr, 0, nk_all, acc, m0, tn);
     store_tile<C, EPI>(p, acc, m0, tn, tid);
   }
-  if (sp.round_need) coop_stage<C::NT>(p, cons_id, sp.q, sp.batch, st_total);
+  if (sp.round_need && sp.gsize == 0) coop_stage<C::NT>(p, p.n_cons, sp.q, sp.batch, st_total);
+  // alternating mode: a consumer with no tile in the last whole round
+  // still copies its shares of the ranges staged before that round
+  if (sp.round_need && sp.gsize > 0)
+    for (int w = n_full_mine; w < sp.n_rounds; ++w) alt_stage<C::NT>(p, cons_id, sp, w);
   if (cons_id >= n_tail_units) return;
   // The K-split unit: tail tile full + tail_idx (unpermuted), K part `part`.
   const int tail_idx = cons_id / p.sk_split;
@@ -977,6 +1033,7 @@ __global__ __launch_bounds__(64 * WAVES, 1) void gemm_kernel(GemmKParams p) {
   sp.batch = 1;
   sp.n_rounds = 0;
   sp.round_need = nullptr;
+  sp.grp = sp.gid = sp.gsize = 0;
   if (p.st_coop) {
     const int ntiles = p.tiles_m * p.tiles_n;
     const int full = (p.sk_split > 1) ? p.sk_full : ntiles;
@@ -985,8 +1042,13 @@ __global__ __launch_bounds__(64 * WAVES, 1) void gemm_kernel(GemmKParams p) {
       build_round_need<C::NT>(p, full, n_rounds, flist, row_key, round_need);
       sp.n_rounds = n_rounds;
       sp.round_need = round_need;
+      if (p.st_coop == 2 && p.xcd_remap && n_rounds >= 1) {
+        sp.gsize = p.n_cons / 2;
+        sp.grp = cons / sp.gsize;
+        sp.gid = cons % sp.gsize;
+      }
     } else {
-      coop_stage<C::NT>(p, cons, sp.q, sp.batch, p.st_nblocks * kPieces);
+      coop_stage<C::NT>(p, p.n_cons, sp.q, sp.batch, p.st_nblocks * kPieces);
     }
   }
   compute_role<C, EPI>(p, cons, smem, perm, flist, sp);

@@ -80,7 +80,9 @@ def ag_gemm(A_shards, A_full, B, C_out, flags, stage_order, epoch: int, gated: b
             num_producers: int = -1, num_cus: int = 0, spin_limit: int = 0, error_word=None,
             stage_counters=None, split_ws=None) -> torch.Tensor:
     """Flag-gated AllGather+GEMM; see include/mk.h mk_ag_gemm.  num_producers
-    -1 (default) stages cooperatively and needs stage_counters (int32
+    -1 (default) stages cooperatively, the two halves of the grid taking
+    turns to copy ahead; -2 stages cooperatively with every workgroup copying
+    an even share before every round.  Both need stage_counters (int32
     [M/128], zeroed once)."""
     _bf16(A_full, "A_full"); _bf16(B, "B"); _bf16(C_out, "C")
     M, K = A_full.shape

@@ -110,7 +110,7 @@ def _ag_case(dev, world=8, shard=256, K=512, N=512, seed=0):
     return cfg, A, B, torch.from_numpy(order)
 
 
-@pytest.mark.parametrize("producers", [-1, 1, 4, 16])
+@pytest.mark.parametrize("producers", [-1, -2, 1, 4, 16])
 def test_ag_gemm_producer_gated(dev, producers):
     _say(f"ag_gemm producers={producers}")
     cfg, A, B, order = _ag_case(dev)
@@ -154,8 +154,9 @@ def test_ag_gemm_epochs_and_orders(dev):
     assert all(torch.equal(outs[0], o) for o in outs[1:])
 
 
-@pytest.mark.parametrize("num_cus,K", [(4, 512), (8, 1024), (3, 2048), (0, 512)])
-def test_ag_gemm_cooperative_staging_capped_grid(dev, num_cus, K):
+@pytest.mark.parametrize("num_cus,K,prod", [(4, 512, -1), (8, 1024, -1), (8, 1024, -2), (16, 512, -1), (3, 2048, -1),
+                                            (0, 512, -1)])
+def test_ag_gemm_cooperative_staging_capped_grid(dev, num_cus, K, prod):
     """Cooperative staging with a capped grid (every workgroup copies many
     pieces and computes several rounds of tiles): staged bytes and flags
     exact, result bit-equal to the ungated GEMM, over several epochs.  With
@@ -163,8 +164,10 @@ def test_ag_gemm_cooperative_staging_capped_grid(dev, num_cus, K):
     whole tiles follow the arrival order (a regression case: a whole tile at
     a permuted position past the split boundary once waited on the split
     flags).  Waits are bounded so a protocol error reports instead of
-    hanging."""
-    _say(f"ag_gemm cooperative num_cus={num_cus} K={K}")
+    hanging.  num_cus 8 and 16 (multiples of the 8 XCDs) run the schedule in
+    which the two halves of the grid take turns copying ahead (-1); -2 the
+    even share."""
+    _say(f"ag_gemm cooperative num_cus={num_cus} K={K} producers={prod}")
     cfg, A, B, order = _ag_case(dev, K=K)
     Ad, Bd = A.to(dev), B.to(dev)
     flags = torch.zeros(cfg.M // 128, dtype=torch.int32, device=dev)
@@ -176,7 +179,7 @@ def test_ag_gemm_cooperative_staging_capped_grid(dev, num_cus, K):
     for epoch in (1, 2, 4):
         A_full = torch.zeros_like(Ad)
         C = torch.empty_like(C_ref)
-        ops.ag_gemm(Ad, A_full, Bd, C, flags, order.to(dev), epoch=epoch, num_producers=-1, num_cus=num_cus,
+        ops.ag_gemm(Ad, A_full, Bd, C, flags, order.to(dev), epoch=epoch, num_producers=prod, num_cus=num_cus,
                     stage_counters=counters, spin_limit=4_000_000, error_word=err)
         torch.cuda.synchronize()
         assert int(err.item()) == 0, "a bounded wait timed out"
@@ -342,3 +345,32 @@ def test_gemm_rejects_operands_beyond_32bit_windows(dev, M, N, K, lda):
     a = capi.GemmArgs(buf.data_ptr(), buf.data_ptr(), buf.data_ptr(), M, N, K, lda, N, N, 0, 256, 0, None, 0)
     rc = capi.lib().mk_gemm(C.byref(a), None)
     assert rc == -2, capi.lib().mk_last_error_string()
+
+
+@pytest.mark.parametrize("prod", [-1, -2])
+def test_ag_gemm_cooperative_staging_full_grid_rounds(dev, prod):
+    """The whole grid over several tile rounds (M 16384, N 2048: 512 tiles of
+    256 x 256), both cooperative schedules, new stage orders and skipped
+    epochs on the same flags and counters: every staged byte and flag exact
+    and the result bit-equal to the ungated GEMM."""
+    _say(f"ag_gemm cooperative full grid producers={prod}")
+    cfg, A, B, _ = _ag_case(dev, shard=2048, K=512, N=2048)
+    Ad, Bd = A.to(dev), B.to(dev)
+    flags = torch.zeros(cfg.M // 128, dtype=torch.int32, device=dev)
+    counters = torch.zeros_like(flags)
+    err = torch.zeros(1, dtype=torch.int32, device=dev)
+    C_ref = torch.empty((cfg.M, cfg.N), dtype=torch.bfloat16, device=dev)
+    ops.ag_gemm(None, Ad, Bd, C_ref, None, None, epoch=1, gated=False, num_producers=0)
+    for epoch, seed in [(1, 31), (2, 32), (5, 33)]:
+        order = torch.from_numpy(wl.stage_order(cfg.M // 128, seed)).to(dev)
+        A_full = torch.zeros_like(Ad)
+        C = torch.empty_like(C_ref)
+        ops.ag_gemm(Ad, A_full, Bd, C, flags, order, epoch=epoch, num_producers=prod, stage_counters=counters,
+                    spin_limit=4_000_000, error_word=err)
+        torch.cuda.synchronize()
+        assert int(err.item()) == 0, "a bounded wait timed out"
+        assert torch.equal(A_full, Ad)
+        assert (flags == epoch).all()
+        assert torch.equal(C, C_ref)
+    rows = slice(4096, 4352)
+    assert rel_fro(C_ref[rows].float().cpu(), gemm_ref(A[rows], B)) < TOL
