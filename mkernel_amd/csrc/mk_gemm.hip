@@ -170,27 +170,61 @@ __device__ void coop_stage(const GemmKParams& p, int stride, int& q, int& batch,
 // Epilogue of one BM x BN tile.  acc[i][j][4a+b] is C[m][n] with
 // m = m0 + wm*WTM + 32i + ml and n (in tile) = wn*WTN + 32j + 8a + 4kg + b.
 // ---------------------------------------------------------------------------
+// s_waitcnt lgkmcnt(0), other counters untouched (gfx9 encoding).
+__device__ __forceinline__ void wait_lgkm_all() { __builtin_amdgcn_s_waitcnt(0xC07F); }
+
+// Row-major store of a wave's WTM x WTN bf16 sub-tile through a private LDS
+// region.  The accumulator layout gives each lane 4 consecutive columns of
+// one row, so a direct store instruction touches 32 rows with 16 bytes each:
+// a 128 KB tile became ~1000 partial-line L2 writes per wave, and the tile
+// epilogue took 13 us of a 200 us tile.  Here each 32-row block goes to LDS
+// as rows of WTN bf16 (row pitch padded by 16 bytes, so the 8-byte writes of
+// the 32 rows spread over the banks), then comes back 16 bytes per lane
+// with consecutive lanes along a row: every store instruction writes whole
+// WTN*2-byte row segments.  The region is the wave's own, so only this
+// wave's LDS ordering matters (lgkmcnt waits); the caller's workgroup
+// barrier must precede the next use of the ring.
+template <class C>
+__device__ __forceinline__ void store_rows(uint16_t* base, int64_t ldc, f32x16 (&acc)[C::FM][C::FN], char* smem,
+                                           int wave, int lane) {
+  constexpr int PITCH = C::WTN * 2 + 16;  // bytes per LDS row
+  constexpr int LPR = C::WTN * 2 / 16;    // lanes per row (16 bytes each)
+  constexpr int RPI = 64 / LPR;           // rows per store instruction
+  static_assert(64 % LPR == 0 && 32 % RPI == 0, "store_rows shape");
+  const int ml = lane & 31, kg = lane >> 5;
+  char* reg = smem + wave * 32 * PITCH;
+  const int rr = lane / LPR, cc = lane % LPR;
+#pragma unroll
+  for (int i = 0; i < C::FM; ++i) {
+#pragma unroll
+    for (int j = 0; j < C::FN; ++j)
+#pragma unroll
+      for (int a = 0; a < 4; ++a) {
+        uint2 w;
+        w.x = pack_bf16x2(acc[i][j][4 * a + 0], acc[i][j][4 * a + 1]);
+        w.y = pack_bf16x2(acc[i][j][4 * a + 2], acc[i][j][4 * a + 3]);
+        *reinterpret_cast<uint2*>(reg + ml * PITCH + (32 * j + 8 * a + 4 * kg) * 2) = w;
+      }
+    wait_lgkm_all();
+#pragma unroll
+    for (int r = 0; r < 32 / RPI; ++r) {
+      const int row = r * RPI + rr;
+      const uint4 v = *reinterpret_cast<const uint4*>(reg + row * PITCH + cc * 16);
+      *reinterpret_cast<uint4*>(base + (int64_t)(i * 32 + row) * ldc + cc * 8) = v;
+    }
+    wait_lgkm_all();  // this block's reads are done before the next block's writes
+  }
+}
+
 template <class C, int EPI>
 __device__ __forceinline__ void store_tile(const GemmKParams& p, f32x16 (&acc)[C::FM][C::FN], int m0, int tn,
-                                           int tid) {
+                                           int tid, char* smem) {
   const int lane = tid & 63, wave = tid >> 6;
   const int wm = wave / C::WN, wn = wave % C::WN;
   const int ml = lane & 31, kg = lane >> 5;
   if constexpr (EPI == kEpiStore) {
-#pragma unroll
-    for (int i = 0; i < C::FM; ++i) {
-      const int m = m0 + wm * C::WTM + i * 32 + ml;
-      uint16_t* crow = p.C + (int64_t)m * p.ldc + tn * C::BN + wn * C::WTN + 4 * kg;
-#pragma unroll
-      for (int j = 0; j < C::FN; ++j)
-#pragma unroll
-        for (int a = 0; a < 4; ++a) {
-          uint2 w;
-          w.x = pack_bf16x2(acc[i][j][4 * a + 0], acc[i][j][4 * a + 1]);
-          w.y = pack_bf16x2(acc[i][j][4 * a + 2], acc[i][j][4 * a + 3]);
-          *reinterpret_cast<uint2*>(crow + j * 32 + 8 * a) = w;
-        }
-    }
+    store_rows<C>(p.C + (int64_t)(m0 + wm * C::WTM) * p.ldc + tn * C::BN + wn * C::WTN, p.ldc, acc, smem, wave, lane);
+    __syncthreads();  // every wave's LDS reads done before the ring is reused
   } else if constexpr (EPI == kEpiSwiGLU) {
     // silu(g) * u in fp32 with silu(g) = g / (1 + e^-g), as the reference
     // computes it (reference src/dispatch_gemm_glu_combine.cu:616-633).
@@ -843,7 +877,7 @@ __device__ void compute_role(const GemmKParams& p, int cons_id, char* smem, cons
     f32x16 acc[C::FM][C::FN];
     int m0, tn;
     tile_body(t, row_perm != nullptr, 0, nk_all, acc, m0, tn);
-    store_tile<C, EPI>(p, acc, m0, tn, tid);
+    store_tile<C, EPI>(p, acc, m0, tn, tid, smem);
   }
   if (sp.round_need && sp.gsize == 0) coop_stage<C::NT>(p, p.n_cons, sp.q, sp.batch, st_total);
   // alternating mode: a consumer with no tile in the last whole round
@@ -885,7 +919,7 @@ __device__ void compute_role(const GemmKParams& p, int cons_id, char* smem, cons
       for (int q2 = 0; q2 < p.sk_split - 1; ++q2)
         __hip_atomic_store(p.sk_flags + slot0 + q2, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
-  store_tile<C, EPI>(p, acc, m0, tn, tid);
+  store_tile<C, EPI>(p, acc, m0, tn, tid, smem);
 }
 
 // Order of row tiles for a gated consumer: ascending by the stage position at
