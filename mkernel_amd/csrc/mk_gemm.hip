@@ -85,8 +85,8 @@ __device__ __forceinline__ void decode_grouped(int t, int tiles_m, int tiles_n, 
 // epilogue a 256-column tile holds 128 gate columns (LDS columns 0..127:
 // gate columns tn*128 ..) and the 128 matching up columns (LDS 128..255:
 // I + tn*128 ..), so every B k-row is fetched as two 256-byte segments.
-// Wave wn's fragment jb reads 32-column LDS block jb*WN + wn (b_block), so
-// fragment jb and jb + FN/2 of one thread hold a gate and its up column.
+// Wave wn's fragments read the LDS blocks b_block gives, so fragment jb and
+// jb + FN/2 of one thread hold a gate and its up column.
 template <class C, int EPI>
 __device__ __forceinline__ int b_col(const GemmKParams& p, int tn, int q) {
   if constexpr (EPI == kEpiSwiGLU) {
@@ -97,11 +97,19 @@ __device__ __forceinline__ int b_col(const GemmKParams& p, int tn, int q) {
   }
 }
 
-// 32-column LDS block that wave wn's B fragment jb reads.
+// 32-column LDS block that wave wn's B fragment jb reads.  With SwiGLU the
+// wave's gate fragments (jb < FN/2) are adjacent blocks of the gate half and
+// its up fragments the same blocks of the up half, so fragment jb and
+// jb + FN/2 of one thread hold a gate column and its up column, and the
+// wave's output columns are contiguous.
 template <class C, int EPI>
 __device__ __forceinline__ int b_block(int wn, int jb) {
-  if constexpr (EPI == kEpiSwiGLU) return jb * C::WN + wn;
-  else return wn * C::FN + jb;
+  if constexpr (EPI == kEpiSwiGLU) {
+    constexpr int H = C::FN / 2;
+    return jb < H ? wn * H + jb : C::WN * H + wn * H + (jb - H);
+  } else {
+    return wn * C::FN + jb;
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -184,20 +192,26 @@ __device__ __forceinline__ void wait_lgkm_all() { __builtin_amdgcn_s_waitcnt(0xC
 // WTN*2-byte row segments.  The region is the wave's own, so only this
 // wave's LDS ordering matters (lgkmcnt waits); the caller's workgroup
 // barrier must precede the next use of the ring.
-template <class C>
+template <class C, int NJ = C::FN>
 __device__ __forceinline__ void store_rows(uint16_t* base, int64_t ldc, f32x16 (&acc)[C::FM][C::FN], char* smem,
                                            int wave, int lane) {
-  constexpr int PITCH = C::WTN * 2 + 16;  // bytes per LDS row
-  constexpr int LPR = C::WTN * 2 / 16;    // lanes per row (16 bytes each)
+  constexpr int W = NJ * 32;              // columns stored per row: accumulator blocks j < NJ
+  constexpr int PITCH = W * 2 + 16;       // bytes per LDS row
+  constexpr int LPR = W * 2 / 16;         // lanes per row (16 bytes each)
   constexpr int RPI = 64 / LPR;           // rows per store instruction
   static_assert(64 % LPR == 0 && 32 % RPI == 0, "store_rows shape");
-  const int ml = lane & 31, kg = lane >> 5;
+  // The lane index goes through an empty asm so that nothing derived from
+  // it is hoisted above the K loop (it would stay live across the loop and
+  // push the loop's operand registers into spills).
+  int l = lane;
+  asm volatile("" : "+v"(l));
+  const int ml = l & 31, kg = l >> 5;
   char* reg = smem + wave * 32 * PITCH;
-  const int rr = lane / LPR, cc = lane % LPR;
+  const int rr = l / LPR, cc = l % LPR;
 #pragma unroll
   for (int i = 0; i < C::FM; ++i) {
 #pragma unroll
-    for (int j = 0; j < C::FN; ++j)
+    for (int j = 0; j < NJ; ++j)
 #pragma unroll
       for (int a = 0; a < 4; ++a) {
         uint2 w;
@@ -227,45 +241,27 @@ __device__ __forceinline__ void store_tile(const GemmKParams& p, f32x16 (&acc)[C
     __syncthreads();  // every wave's LDS reads done before the ring is reused
   } else if constexpr (EPI == kEpiSwiGLU) {
     // silu(g) * u in fp32 with silu(g) = g / (1 + e^-g), as the reference
-    // computes it (reference src/dispatch_gemm_glu_combine.cu:616-633).
+    // computes it (reference src/dispatch_gemm_glu_combine.cu:616-633),
+    // in place in the gate accumulators; a wave's gate blocks are adjacent
+    // output columns (b_block), so the rows go out as whole segments.
 #pragma unroll
-    for (int i = 0; i < C::FM; ++i) {
-      const int m = m0 + wm * C::WTM + i * 32 + ml;
-      uint16_t* crow = p.C + (int64_t)m * p.ldc + tn * (C::BN / 2) + 4 * kg;
+    for (int i = 0; i < C::FM; ++i)
 #pragma unroll
       for (int j = 0; j < C::FN / 2; ++j)
 #pragma unroll
-        for (int a = 0; a < 4; ++a) {
-          float o[4];
-#pragma unroll
-          for (int b = 0; b < 4; ++b) {
-            const float g = acc[i][j][4 * a + b];
-            const float u = acc[i][j + C::FN / 2][4 * a + b];
-            o[b] = (g / (1.0f + __expf(-g))) * u;
-          }
-          uint2 w;
-          w.x = pack_bf16x2(o[0], o[1]);
-          w.y = pack_bf16x2(o[2], o[3]);
-          *reinterpret_cast<uint2*>(crow + b_block<C, EPI>(wn, j) * 32 + 8 * a) = w;
+        for (int v = 0; v < 16; ++v) {
+          const float g = acc[i][j][v];
+          acc[i][j][v] = (g / (1.0f + __expf(-g))) * acc[i][j + C::FN / 2][v];
         }
-    }
+    store_rows<C, C::FN / 2>(p.C + (int64_t)(m0 + wm * C::WTM) * p.ldc + tn * (C::BN / 2) + wn * (C::WTN / 2), p.ldc,
+                             acc, smem, wave, lane);
+    __syncthreads();  // every wave's LDS reads done before the ring is reused
   } else {  // kEpiReduce
     const bool owned = m0 >= p.rs_own_row0 && m0 < p.rs_own_row0 + p.rs_own_rows;
     if (!owned) {
-#pragma unroll
-      for (int i = 0; i < C::FM; ++i) {
-        const int m = m0 + wm * C::WTM + i * 32 + ml;
-        uint16_t* crow = p.C + (int64_t)m * p.ldc + tn * C::BN + wn * C::WTN + 4 * kg;
-#pragma unroll
-        for (int j = 0; j < C::FN; ++j)
-#pragma unroll
-          for (int a = 0; a < 4; ++a) {
-            uint2 w;
-            w.x = pack_bf16x2(acc[i][j][4 * a + 0], acc[i][j][4 * a + 1]);
-            w.y = pack_bf16x2(acc[i][j][4 * a + 2], acc[i][j][4 * a + 3]);
-            *reinterpret_cast<uint2*>(crow + j * 32 + 8 * a) = w;
-          }
-      }
+      store_rows<C>(p.C + (int64_t)(m0 + wm * C::WTM) * p.ldc + tn * C::BN + wn * C::WTN, p.ldc, acc, smem, wave,
+                    lane);
+      __syncthreads();  // every wave's LDS reads done before the ring is reused
     } else {
       const int lr0 = m0 - p.rs_own_row0;  // first row inside the owned slice
       if (p.rs_flags) {
@@ -308,26 +304,13 @@ __device__ __forceinline__ void store_tile(const GemmKParams& p, f32x16 (&acc)[C
               acc[i][j][4 * a + 3] += bf16_hi(v[i][j][a].y);
             }
       }
-#pragma unroll
-      for (int i = 0; i < C::FM; ++i) {
-        const int lr = lr0 + wm * C::WTM + i * 32 + ml;
-        uint16_t* orow = p.rs_out + (int64_t)lr * p.ldc + tn * C::BN + wn * C::WTN + 4 * kg;
-#pragma unroll
-        for (int j = 0; j < C::FN; ++j)
-#pragma unroll
-          for (int a = 0; a < 4; ++a) {
-            uint2 w;
-            w.x = pack_bf16x2(acc[i][j][4 * a + 0], acc[i][j][4 * a + 1]);
-            w.y = pack_bf16x2(acc[i][j][4 * a + 2], acc[i][j][4 * a + 3]);
-            *reinterpret_cast<uint2*>(orow + j * 32 + 8 * a) = w;
-          }
-      }
+      store_rows<C>(p.rs_out + (int64_t)(lr0 + wm * C::WTM) * p.ldc + tn * C::BN + wn * C::WTN, p.ldc, acc, smem,
+                    wave, lane);
+      __syncthreads();  // every wave's LDS reads done before the ring is reused
       if (p.ar_done) {
         // all-reduce: publish the finished tile (the broadcast hand-off).
-        // The tile's 8-byte row pieces are plain stores (written through
-        // piecewise they would cost a memory write per piece), so the flag
-        // is a release store: one L2 write-back per tile.
-        __syncthreads();
+        // The tile's rows are plain stores, so the flag is a release store:
+        // one L2 write-back per tile.
         if (tid == 0) publish_flag(p.ar_done + (m0 / C::BM) * p.tiles_n + tn, p.epoch);
       }
     }
@@ -519,7 +502,7 @@ __device__ __forceinline__ void add_partial(const float* src, f32x16 (&acc)[C::F
 // epilogue.  Every round then keeps all consumers busy.
 // ---------------------------------------------------------------------------
 template <class C, int EPI>
-__device__ void compute_role(const GemmKParams& p, int cons_id, char* smem, const int* row_perm,
+__device__ __forceinline__ void compute_role(const GemmKParams& p, int cons_id, char* smem, const int* row_perm,
                              const uint16_t* full_list, StagePlan& sp) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
