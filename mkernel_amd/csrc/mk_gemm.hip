@@ -230,6 +230,77 @@ __device__ __forceinline__ void store_rows(uint16_t* base, int64_t ldc, f32x16 (
   }
 }
 
+// Reduce epilogue of an owned tile, row-major: each 32-row block of the
+// wave's fp32 accumulators goes through the wave's LDS region (rows of WTN
+// fp32, pitch padded by 16 bytes) and comes back 8 columns per lane with
+// consecutive lanes along a row; the lane then loads the same 8 columns of
+// every peer's bf16 partial (16 bytes per peer: whole row segments per
+// instruction, 4 peers' loads in flight), adds them in rank order in fp32
+// (deterministic, one rounding) and stores 16 bytes of the owned output.
+// In the accumulator layout every load and store instruction would touch
+// 32 rows with 8 bytes each.
+template <class C>
+__device__ __forceinline__ void reduce_rows(const GemmKParams& p, f32x16 (&acc)[C::FM][C::FN], int lrow0, int col0,
+                                            char* smem, int wave, int lane) {
+  constexpr int PITCH = C::WTN * 4 + 16;  // bytes per LDS row (fp32)
+  constexpr int LPR = C::WTN / 8;         // lanes per row (8 columns each)
+  constexpr int RPI = 64 / LPR;           // rows per instruction
+  constexpr int kPeers = 4;               // peer loads in flight per lane
+  static_assert(64 % LPR == 0 && 32 % RPI == 0, "reduce_rows shape");
+  int l = lane;
+  asm volatile("" : "+v"(l));  // keep lane-derived addressing below the K loop
+  const int ml = l & 31, kg = l >> 5;
+  char* reg = smem + wave * 32 * PITCH;
+  const int rr = l / LPR, cc = l % LPR;
+  const int64_t peer_stride = (int64_t)p.rs_own_rows * p.ldc;
+  const int np = p.rs_npeers;
+#pragma unroll
+  for (int i = 0; i < C::FM; ++i) {
+#pragma unroll
+    for (int j = 0; j < C::FN; ++j)
+#pragma unroll
+      for (int a = 0; a < 4; ++a) {
+        f32x4 w;
+#pragma unroll
+        for (int b = 0; b < 4; ++b) w[b] = acc[i][j][4 * a + b];
+        *reinterpret_cast<f32x4*>(reg + ml * PITCH + (32 * j + 8 * a + 4 * kg) * 4) = w;
+      }
+    wait_lgkm_all();
+    for (int r = 0; r < 32 / RPI; ++r) {
+      const int row = r * RPI + rr;
+      const f32x4 lo = *reinterpret_cast<const f32x4*>(reg + row * PITCH + cc * 32);
+      const f32x4 hi = *reinterpret_cast<const f32x4*>(reg + row * PITCH + cc * 32 + 16);
+      float x[8] = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+      const uint16_t* src = p.rs_recv + (int64_t)(lrow0 + i * 32 + row) * p.ldc + col0 + cc * 8;
+      int q = 0;
+      for (; q + kPeers <= np; q += kPeers) {
+        uint4 v[kPeers];
+#pragma unroll
+        for (int u = 0; u < kPeers; ++u) v[u] = *reinterpret_cast<const uint4*>(src + (q + u) * peer_stride);
+#pragma unroll
+        for (int u = 0; u < kPeers; ++u) {
+          x[0] += bf16_lo(v[u].x); x[1] += bf16_hi(v[u].x);
+          x[2] += bf16_lo(v[u].y); x[3] += bf16_hi(v[u].y);
+          x[4] += bf16_lo(v[u].z); x[5] += bf16_hi(v[u].z);
+          x[6] += bf16_lo(v[u].w); x[7] += bf16_hi(v[u].w);
+        }
+      }
+      for (; q < np; ++q) {
+        const uint4 v = *reinterpret_cast<const uint4*>(src + q * peer_stride);
+        x[0] += bf16_lo(v.x); x[1] += bf16_hi(v.x);
+        x[2] += bf16_lo(v.y); x[3] += bf16_hi(v.y);
+        x[4] += bf16_lo(v.z); x[5] += bf16_hi(v.z);
+        x[6] += bf16_lo(v.w); x[7] += bf16_hi(v.w);
+      }
+      uint4 o;
+      o.x = pack_bf16x2(x[0], x[1]); o.y = pack_bf16x2(x[2], x[3]);
+      o.z = pack_bf16x2(x[4], x[5]); o.w = pack_bf16x2(x[6], x[7]);
+      *reinterpret_cast<uint4*>(p.rs_out + (int64_t)(lrow0 + i * 32 + row) * p.ldc + col0 + cc * 8) = o;
+    }
+    wait_lgkm_all();  // this block's reads are done before the next block's writes
+  }
+}
+
 template <class C, int EPI>
 __device__ __forceinline__ void store_tile(const GemmKParams& p, f32x16 (&acc)[C::FM][C::FN], int m0, int tn,
                                            int tid, char* smem) {
@@ -272,40 +343,7 @@ __device__ __forceinline__ void store_tile(const GemmKParams& p, f32x16 (&acc)[C
                      p.rs_npeers * per, p.epoch, p.spin_limit, p.err);
         __syncthreads();
       }
-      // Fold the peers' bf16 partials into the fp32 accumulators, peer by
-      // peer in rank order (deterministic).  All of one peer's loads are
-      // issued before any is consumed (one memory latency per peer, not per
-      // element); buffer loads keep the per-element offsets as immediates.
-      const int64_t peer_stride = (int64_t)p.rs_own_rows * p.ldc;
-      uint32_t voff[C::FM];
-#pragma unroll
-      for (int i = 0; i < C::FM; ++i)
-        voff[i] = (uint32_t)(((wm * C::WTM + i * 32 + ml) * p.ldc + tn * C::BN + wn * C::WTN + 4 * kg) * 2);
-      for (int q = 0; q < p.rs_npeers; ++q) {
-        const __amdgpu_buffer_rsrc_t r =
-            make_rsrc(p.rs_recv + q * peer_stride + (int64_t)lr0 * p.ldc, (uint32_t)(C::BM * p.ldc * 2));
-        uint2 v[C::FM][C::FN][4];
-#pragma unroll
-        for (int i = 0; i < C::FM; ++i)
-#pragma unroll
-          for (int j = 0; j < C::FN; ++j)
-#pragma unroll
-            for (int a = 0; a < 4; ++a)
-              v[i][j][a] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(r, voff[i] + (j * 32 + 8 * a) * 2, 0, 0));
-#pragma unroll
-        for (int i = 0; i < C::FM; ++i)
-#pragma unroll
-          for (int j = 0; j < C::FN; ++j)
-#pragma unroll
-            for (int a = 0; a < 4; ++a) {
-              acc[i][j][4 * a + 0] += bf16_lo(v[i][j][a].x);
-              acc[i][j][4 * a + 1] += bf16_hi(v[i][j][a].x);
-              acc[i][j][4 * a + 2] += bf16_lo(v[i][j][a].y);
-              acc[i][j][4 * a + 3] += bf16_hi(v[i][j][a].y);
-            }
-      }
-      store_rows<C>(p.rs_out + (int64_t)(lr0 + wm * C::WTM) * p.ldc + tn * C::BN + wn * C::WTN, p.ldc, acc, smem,
-                    wave, lane);
+      reduce_rows<C>(p, acc, lr0 + wm * C::WTM, tn * C::BN + wn * C::WTN, smem, wave, lane);
       __syncthreads();  // every wave's LDS reads done before the ring is reused
       if (p.ar_done) {
         // all-reduce: publish the finished tile (the broadcast hand-off).
