@@ -508,7 +508,7 @@ __device__ __forceinline__ void put_partial(float* dst, f32x16 (&acc)[C::FM][C::
 #pragma unroll
         for (int b = 0; b < 4; ++b) v[b] = acc[i][j][4 * a + b];
         __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, v), r, tid * 16,
-                                               ((i * C::FN + j) * 4 + a) * C::NT * 16, 0x12 /* SC1 | NT */);
+                                               ((i * C::FN + j) * 4 + a) * C::NT * 16, 0x10 /* SC1 */);
       }
 }
 
