@@ -287,3 +287,28 @@ def test_ffn_combine_ragged_extremes(dev):
     routed = torch.zeros(cfg.tokens, dtype=torch.bool)
     routed[[7, 200]] = True
     assert (y.cpu()[~routed] == 0).all()
+
+
+@pytest.mark.parametrize("tile_n", [256, 512])
+def test_swiglu_epilogue_values(dev, tile_n):
+    """The SwiGLU epilogue on exactly known gate/up values: one-hot rows of A
+    select rows of one expert's W1, so h = W1 rows exactly and act must be
+    bf16(silu(g) * u) of those bf16 values, including large gates (e^-g
+    overflows to inf: silu -> -0 / silu -> g), zero and tiny gates.  Every
+    element within one bf16 rounding step of the fp32 oracle."""
+    _say(f"moe swiglu epilogue values tile_n={tile_n}")
+    K, I = 128, 512
+    g = torch.linspace(-100.0, 100.0, K * I).reshape(K, I)
+    g[:, :8] = torch.tensor([0.0, -0.0, 1e-30, -1e-30, 88.0, -88.0, 1e4, -1e4])
+    u = wl.randn_bf16((K, I), 41).float()
+    w1 = torch.cat([g, u], dim=1).to(torch.bfloat16).unsqueeze(0)  # [1, K, 2I]
+    A = torch.zeros((128, K), dtype=torch.bfloat16)
+    A[torch.arange(128), torch.arange(128) % K] = 1.0
+    rb_expert = torch.zeros(1, dtype=torch.int32, device=dev)
+    act = torch.empty((128, I), dtype=torch.bfloat16, device=dev)
+    ops.moe_grouped_gemm(A.to(dev), w1.to(dev), act, rb_expert=rb_expert, mode=1, split_ws=False, tile_n=tile_n)
+    torch.cuda.synchronize()
+    ref = om.silu_mul(w1[0, :, :I].float(), w1[0, :, I:].float())
+    got = act.cpu().float()
+    assert torch.isfinite(got).all()
+    assert torch.allclose(got, ref, rtol=2 ** -7, atol=1e-30)
