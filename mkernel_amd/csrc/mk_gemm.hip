@@ -513,28 +513,52 @@ __device__ __forceinline__ void put_partial(float* dst, f32x16 (&acc)[C::FM][C::
 }
 
 template <class C>
-__device__ __forceinline__ void add_partial(const float* src, f32x16 (&acc)[C::FM][C::FN], int tid) {
-  // Loads go out in groups of kGroup with every load of a group issued
-  // before its adds: with the 128 accumulators live the compiler would
-  // otherwise issue one load at a time and pay one memory latency per load
-  // (22 us for a 128 x 512 tile measured).
-  constexpr int kUnits = C::FM * C::FN * 4, kGroup = 8;
-  static_assert(kUnits % kGroup == 0, "add_partial grouping");
-  const __amdgpu_buffer_rsrc_t r = make_rsrc(src, (uint32_t)(C::BM * C::BN * 4));
+__device__ __forceinline__ void add_partial(const float* src, f32x16 (&acc)[C::FM][C::FN], int tid, char* smem) {
+  // The partial comes in through the (idle) LDS ring by DMA, kChunk units
+  // of 16 bytes per thread at a time, two chunks in flight: register-staged
+  // loads were limited to 8 in flight per thread by the 128 live
+  // accumulators (15 us for a 256 KB partial), the DMA needs no registers.
+  // Unit n of thread t sits at (n * NT + t) * 16 in the partial, so a chunk
+  // is one contiguous range and each thread reads its own 16-byte slots
+  // back (consecutive lanes, consecutive addresses: no bank conflicts).
+  constexpr int kUnits = C::FM * C::FN * 4, kChunk = 4, kChunks = kUnits / kChunk;
+  constexpr uint32_t CHUNK = kChunk * C::NT * 16;          // bytes per chunk
+  constexpr int PER_WAVE = CHUNK / 1024 / C::WAVES;          // 1 KB DMA instructions per wave per chunk
+  static_assert(kUnits % kChunk == 0 && PER_WAVE >= 1 && 2 * CHUNK <= C::LDS_BYTES, "add_partial chunks");
+  const int lane = tid & 63;
+  const uint32_t wave_u = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)smem;
+  const u32x4_t r = make_rsrc_v(src, (uint32_t)(C::BM * C::BN * 4));
+  auto issue = [&](int c) {
+    const uint32_t buf = lds0 + (uint32_t)(c & 1) * CHUNK;
 #pragma unroll
-  for (int g = 0; g < kUnits; g += kGroup) {
-    f32x4 v[kGroup];
-#pragma unroll
-    for (int u = 0; u < kGroup; ++u)
-      v[u] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, tid * 16, (g + u) * C::NT * 16, 0));
-#pragma unroll
-    for (int u = 0; u < kGroup; ++u) {
-      const int n = g + u, i = n / (C::FN * 4), j = (n / 4) % C::FN, a = n % 4;
-#pragma unroll
-      for (int b = 0; b < 4; ++b) acc[i][j][4 * a + b] += v[u][b];
+    for (int i = 0; i < PER_WAVE; ++i) {
+      const uint32_t blk = (wave_u * PER_WAVE + i) * 1024;
+      dma16(r, buf + blk, (uint32_t)lane * 16, (uint32_t)c * CHUNK + blk);
     }
-    __builtin_amdgcn_sched_barrier(0);  // keep the next group's loads after these adds
+  };
+  issue(0);
+  if (kChunks > 1) issue(1);
+#pragma unroll
+  for (int c = 0; c < kChunks; ++c) {
+    if (c + 1 < kChunks) wait_vm<PER_WAVE>();  // chunk c landed (chunk c+1 may be in flight)
+    else wait_vm<0>();
+    __syncthreads();
+    const char* buf = smem + (c & 1) * CHUNK;
+#pragma unroll
+    for (int u = 0; u < kChunk; ++u) {
+      const int n = c * kChunk + u, i = n / (C::FN * 4), j = (n / 4) % C::FN, a = n % 4;
+      const f32x4 v = *reinterpret_cast<const f32x4*>(buf + (u * C::NT + tid) * 16);
+#pragma unroll
+      for (int b = 0; b < 4; ++b) acc[i][j][4 * a + b] += v[b];
+    }
+    if (c + 2 < kChunks) {
+      wait_lgkm_all();
+      __syncthreads();  // every thread is done with this buffer
+      issue(c + 2);
+    }
   }
+  __syncthreads();  // the ring is free again for the epilogue
 }
 
 // ---------------------------------------------------------------------------
@@ -944,7 +968,7 @@ __device__ __forceinline__ void compute_role(const GemmKParams& p, int cons_id, 
         wait_flags<1>([&](int) { return p.sk_flags + slot0 + q2; }, 1, 1u, p.spin_limit, p.err);
     __syncthreads();
     for (int q2 = 0; q2 < p.sk_split - 1; ++q2)
-      add_partial<C>(p.sk_ws + (int64_t)(slot0 + q2) * (C::BM * C::BN), acc, tid);
+      add_partial<C>(p.sk_ws + (int64_t)(slot0 + q2) * (C::BM * C::BN), acc, tid, smem);
     if (tid == 0)
       for (int q2 = 0; q2 < p.sk_split - 1; ++q2)
         __hip_atomic_store(p.sk_flags + slot0 + q2, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
