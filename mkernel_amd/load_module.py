@@ -31,7 +31,7 @@ import torch
 
 from . import ops
 
-_DEFAULT_PRODUCERS = -1  # cooperative staging by every workgroup
+_DEFAULT_PRODUCERS = -1  # cooperative staging by the compute workgroups
 _COUNTERS: dict = {}
 
 
@@ -147,11 +147,12 @@ def _ag_module():
         producer role copies each 128-row tile into ``A.data_`` and publishes
         ``barrier`` word tile = epoch).  Pass ``A_recv=None`` when ``A.data_``
         is filled by someone else who also publishes the flags.  Producers:
-        ``num_intra_comm_override`` if > 0, else 32.  ``active_sms`` caps the
-        grid (0 or >= CU count: every CU).  The default (-1) stages
-        cooperatively: every workgroup copies its share first.  ``stage_order`` (int32 device
-        tensor, optional) is the tile publication order the compute role
-        follows."""
+        ``num_intra_comm_override`` dedicated producer workgroups if > 0,
+        else cooperative staging: the compute workgroups copy the tiles
+        between their tile rounds, the two XCD halves of the grid taking
+        turns to copy ahead.  ``active_sms`` caps the grid (0 or >= CU
+        count: every CU).  ``stage_order`` (int32 device tensor, optional)
+        is the tile publication order the compute role follows."""
         Af = _data(A)
         M, K = Af.shape
         src = _data(A_recv) if A_recv is not None else None
