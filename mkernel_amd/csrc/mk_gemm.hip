@@ -561,6 +561,30 @@ __device__ __forceinline__ void add_partial(const float* src, f32x16 (&acc)[C::F
   __syncthreads();  // the ring is free again for the epilogue
 }
 
+// The fp32 partial of another workgroup added into this thread's
+// accumulators, per thread with no workgroup barrier (for a subset of the
+// waves): loads in groups of 8, each group's loads issued before its adds.
+template <class C>
+__device__ __forceinline__ void add_partial_regs(const float* src, f32x16 (&acc)[C::FM][C::FN], int tid) {
+  constexpr int kUnits = C::FM * C::FN * 4, kGroup = 8;
+  static_assert(kUnits % kGroup == 0, "add_partial_regs grouping");
+  const __amdgpu_buffer_rsrc_t r = make_rsrc(src, (uint32_t)(C::BM * C::BN * 4));
+#pragma unroll
+  for (int g = 0; g < kUnits; g += kGroup) {
+    f32x4 v[kGroup];
+#pragma unroll
+    for (int u = 0; u < kGroup; ++u)
+      v[u] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, tid * 16, (g + u) * C::NT * 16, 0));
+#pragma unroll
+    for (int u = 0; u < kGroup; ++u) {
+      const int n = g + u, i = n / (C::FN * 4), j = (n / 4) % C::FN, a = n % 4;
+#pragma unroll
+      for (int b = 0; b < 4; ++b) acc[i][j][4 * a + b] += v[u][b];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Compute role
 //
@@ -947,6 +971,36 @@ __device__ __forceinline__ void compute_role(const GemmKParams& p, int cons_id, 
   f32x16 acc[C::FM][C::FN];
   int m0, tn;
   tile_body(full + tail_idx, false, k0, nk, acc, m0, tn);
+  if (C::WM == 2 && p.sk_split == 2 && EPI != kEpiReduce) {
+    // Two-way split: the parts swap half tiles.  Part q finalizes the rows
+    // of the waves with wm == q (rows q*WTM .. q*WTM + WTM - 1): the other
+    // waves write their fp32 partial to this part's slot, and after the
+    // other part's flag the owning waves add its partial and store their
+    // rows.  Both workgroups of the tile finish together, each moving half
+    // of the tile (one owner folding the whole tile measured ~33 us while
+    // the contributor sat idle).  Each element is the sum of the same two
+    // fp32 terms as with one owner (a two-term sum does not depend on order).
+    const int slot_out = tail_idx * 2 + part, slot_in = tail_idx * 2 + (1 - part);
+    const bool own_rows = wm == part;
+    if (!own_rows) put_partial<C>(p.sk_ws + (int64_t)slot_out * (C::BM * C::BN), acc, tid);
+    // write-through stores performed at agent scope, then a relaxed flag
+    // (the protocol of copy_wt: no L2 write-back needed)
+    wait_vmem_all();
+    __syncthreads();
+    if (tid == 0) {
+      __hip_atomic_store(p.sk_flags + slot_out, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      wait_flags<1>([&](int) { return p.sk_flags + slot_in; }, 1, 1u, p.spin_limit, p.err);
+    }
+    __syncthreads();
+    if (own_rows) {
+      // two fp32 terms: the sum is the same whichever part adds
+      add_partial_regs<C>(p.sk_ws + (int64_t)slot_in * (C::BM * C::BN), acc, tid);
+      store_tile<C, EPI>(p, acc, m0, tn, tid, smem);
+    }
+    __syncthreads();  // the partial is read: clear its flag for the next launch
+    if (tid == 0) __hip_atomic_store(p.sk_flags + slot_in, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return;
+  }
   if (part > 0) {
     // K-split contributor: publish the partial for part 0 of this tile.
     const int slot = tail_idx * (p.sk_split - 1) + part - 1;

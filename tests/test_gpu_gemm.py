@@ -374,3 +374,37 @@ def test_ag_gemm_cooperative_staging_full_grid_rounds(dev, prod):
         assert torch.equal(C, C_ref)
     rows = slice(4096, 4352)
     assert rel_fro(C_ref[rows].float().cpu(), gemm_ref(A[rows], B)) < TOL
+
+
+@pytest.mark.parametrize("M,N,K,cus,waves", [(2048, 1536, 2048, 32, 8),   # 48 tiles on 32: 16 split 2 ways
+                                             (2048, 1536, 2048, 40, 8),   # 8 tail tiles split 4 ways (40 // 8 > 4)
+                                             (2048, 1536, 2048, 36, 8),   # 12 tail tiles split 3 ways
+                                             (2048, 2560, 1024, 64, 8),   # 80 tiles: 16 split 4 ways
+                                             (2048, 1536, 2048, 32, 4),   # 4-wave workgroups, 2-way
+                                             (1024, 1024, 4096, 8, 8)])   # 16 tiles on 8: no tail
+def test_gemm_split_tail_exchange(dev, M, N, K, cus, waves):
+    """K-split tails at capped grids: the 2-way split swaps half tiles
+    between its two workgroups, wider splits fold into one owner.  Against
+    the oracle, against the unsplit GEMM (fp32 rounding only), identical
+    across three launches on one workspace, flags left zeroed."""
+    _say(f"gemm split exchange M={M} N={N} K={K} cus={cus} waves={waves}")
+    A = wl.randn_bf16((M, K), 31, K ** -0.5).to(dev)
+    B = wl.randn_bf16((K, N), 32, K ** -0.5).to(dev)
+    ws = torch.zeros(int(ops.capi.lib().mk_query_workspace_bytes(0, M, N, K)), dtype=torch.uint8, device=dev)
+    plain = ops.gemm(A, B, tile_m=256, num_cus=cus, waves=waves, split_ws=False)
+    outs = [ops.gemm(A, B, tile_m=256, num_cus=cus, waves=waves, split_ws=ws) for _ in range(3)]
+    torch.cuda.synchronize()
+    ref = gemm_ref(A.cpu(), B.cpu())
+    assert rel_fro(outs[0].float().cpu(), ref) < TOL
+    assert torch.allclose(outs[0].float(), plain.float(), rtol=2 ** -7, atol=1e-5)
+    assert all(torch.equal(outs[0], o) for o in outs[1:])
+    assert int(ws[:4096].view(torch.int32).abs().sum()) == 0, "split flags not left zeroed"
+
+
+def test_gemm_split_tail_exchange_identity_exact(dev):
+    """I @ X through a 2-way split tail is exact: each half tile's sum is the
+    unsplit sum (products by 0 and 1 are exact in fp32)."""
+    n = 2048
+    I = torch.eye(n, dtype=torch.bfloat16, device=dev)
+    X = wl.randn_bf16((n, 1536), 33).to(dev)
+    assert torch.equal(ops.gemm(I, X, tile_m=256, num_cus=32).cpu(), X.cpu())

@@ -312,3 +312,26 @@ def test_swiglu_epilogue_values(dev, tile_n):
     got = act.cpu().float()
     assert torch.isfinite(got).all()
     assert torch.allclose(got, ref, rtol=2 ** -7, atol=1e-30)
+
+
+def test_gemm1_swiglu_split_tail_exchange(dev):
+    """Grouped GEMM1 + SwiGLU with a capped grid so the tail round is split
+    2 ways (half-tile swap): against the oracle, bit-equal across repeated
+    launches, and within rounding of the unsplit launch."""
+    _say("moe gemm1+swiglu split exchange")
+    tokens, ids, gates, w1, w2, idx, d = _setup(dev, WIDE)
+    post = om.permute_ref(tokens, idx["pull_indices"])
+    ntiles = (idx["R_pad"] // 128) * (2 * WIDE.I // 512)
+    # a grid whose tail (ntiles % cus tiles) the library splits 2 ways: cus / tail in [2, 3)
+    cus = next(c for c in range(2, ntiles) if ntiles % c and 2 <= c // (ntiles % c) < 3)
+    outs = []
+    for split in (None, None, False):
+        act = torch.empty((idx["R_pad"], WIDE.I), dtype=torch.bfloat16, device=dev)
+        ops.moe_grouped_gemm(post.to(dev), w1.to(dev), act, rb_expert=d["rb_expert"], mode=1, split_ws=split,
+                             tile_n=512, num_cus=cus)
+        outs.append(act)
+    torch.cuda.synchronize()
+    ref_act, _ = om.ffn_ref(post, w1, w2, idx["padded_tokens_per_expert"], WIDE.I)
+    assert rel_fro(outs[0].float().cpu(), ref_act) < TOL
+    assert torch.equal(outs[0], outs[1])
+    assert torch.allclose(outs[0].float(), outs[2].float(), rtol=2 ** -6, atol=1e-3)
