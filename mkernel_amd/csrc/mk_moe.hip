@@ -35,16 +35,30 @@ hipError_t launch_permute(const PermuteKParams& p, hipStream_t stream) {
 }
 
 // One workgroup per source token; each thread owns 8 contiguous columns.
+// The token's (row, weight) pairs are loaded once per thread, before the
+// column loop (at most kMaxSlots of them; more fall back to the slot loop),
+// and all of a chunk's row loads are issued before they are summed: the
+// kernel is latency-bound, and the dependent owner -> slot -> row -> data
+// chain per column chunk made it so.  Sums stay in slot order
+// (deterministic, bit-identical to the plain loop).
 __global__ __launch_bounds__(kThreads) void combine_kernel(CombineKParams p) {
+  constexpr int kMaxSlots = 8;
   const int64_t t = blockIdx.x;
   const int s0 = p.owner_offset[t], s1 = p.owner_offset[t + 1];
+  const int n = s1 - s0;
   const int64_t vec = p.H / 8;
+  int rows[kMaxSlots];
+  float wts[kMaxSlots];
+  const bool few = n <= kMaxSlots;
+#pragma unroll
+  for (int k = 0; k < kMaxSlots; ++k)
+    if (few && k < n) rows[k] = p.slot_to_row[s0 + k];
+#pragma unroll
+  for (int k = 0; k < kMaxSlots; ++k)
+    if (few && k < n) wts[k] = p.row_weight[rows[k]];
   for (int64_t c = threadIdx.x; c < vec; c += kThreads) {
     float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    for (int s = s0; s < s1; ++s) {
-      const int row = p.slot_to_row[s];
-      const float w = p.row_weight[row];
-      const uint4 v = *reinterpret_cast<const uint4*>(p.y_expert + (int64_t)row * p.H + c * 8);
+    auto add = [&](float w, const uint4& v) {
       acc[0] += w * bf16_lo(v.x);
       acc[1] += w * bf16_hi(v.x);
       acc[2] += w * bf16_lo(v.y);
@@ -53,6 +67,20 @@ __global__ __launch_bounds__(kThreads) void combine_kernel(CombineKParams p) {
       acc[5] += w * bf16_hi(v.z);
       acc[6] += w * bf16_lo(v.w);
       acc[7] += w * bf16_hi(v.w);
+    };
+    if (few) {
+      uint4 v[kMaxSlots];
+#pragma unroll
+      for (int k = 0; k < kMaxSlots; ++k)
+        if (k < n) v[k] = *reinterpret_cast<const uint4*>(p.y_expert + (int64_t)rows[k] * p.H + c * 8);
+#pragma unroll
+      for (int k = 0; k < kMaxSlots; ++k)
+        if (k < n) add(wts[k], v[k]);
+    } else {
+      for (int s = s0; s < s1; ++s) {
+        const int row = p.slot_to_row[s];
+        add(p.row_weight[row], *reinterpret_cast<const uint4*>(p.y_expert + (int64_t)row * p.H + c * 8));
+      }
     }
     if (p.out_dtype == 0) {
       float4* o = reinterpret_cast<float4*>(static_cast<float*>(p.y_out) + t * p.H + c * 8);
