@@ -300,7 +300,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU's share of the path; runs on more than one GPU are not part of this "
-              "build (see DESIGN.md for how the path shards)", file=sys.stderr)
+              "build: each config is already one rank's share of an 8-GPU job, measured at its real shape on one GPU", file=sys.stderr)
         sys.exit(2)
     if not torch.cuda.is_available():
         print("bench.py needs an MI355X GPU", file=sys.stderr)
