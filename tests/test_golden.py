@@ -1,0 +1,79 @@
+"""The CPU oracle and the host-side C++ index builder against the committed
+known-answer vectors (tests/golden/known_answers.npz, written by
+tests/golden/make_fixtures.py).  No GPU."""
+from pathlib import Path
+
+import numpy as np
+import torch
+
+from oracle import moe as om
+from oracle.gemm import gemm_bruteforce, gemm_ref, gemm_rs_ref, rel_fro
+
+F = np.load(Path(__file__).resolve().parent / "golden" / "known_answers.npz")
+INDEX_KEYS = ("padded_tokens_per_expert", "pull_indices", "row_weight", "owner_offset", "slot_to_row")
+
+
+def _bf(a, scale=1):
+    return (torch.from_numpy(a).float() / scale).to(torch.bfloat16)
+
+
+def moe_inputs():
+    T, H, I, E, K, EP, RANK = (int(v) for v in F["moe_dims"])
+    n_local = E // EP
+    return dict(T=T, H=H, I=I, e0=RANK * n_local, n_local=n_local, ids=F["moe_topk_ids"], gates=F["moe_gates"],
+                tokens=_bf(F["moe_tokens_x2"], 2), w1=_bf(F["moe_w1_x2"], 2), w2=_bf(F["moe_w2_x16"], 16))
+
+
+def test_gemm_known_answer():
+    A, B = _bf(F["gemm_A"]), _bf(F["gemm_B"])
+    C = torch.from_numpy(F["gemm_C"]).float()
+    assert torch.equal(gemm_ref(A, B), C)
+    assert torch.equal(gemm_bruteforce(A[:8], B[:, :8]), C[:8, :8])
+
+
+def test_gemm_rs_known_answer():
+    world, rank = (int(v) for v in F["rs_world_rank"])
+    _, owned = gemm_rs_ref(_bf(F["rs_A"]), _bf(F["rs_B"]), _bf(F["rs_peers"]), rank, world)
+    assert torch.equal(owned, torch.from_numpy(F["rs_owned"]).float())
+
+
+def test_moe_indices_known_answer():
+    m = moe_inputs()
+    # the hand-shaped routing: expert 2 gets t % 4 == 0 and t % 8 == 2, expert 3 gets t % 4 == 1 and t % 8 == 2
+    assert F["moe_padded_tokens_per_expert"].tolist() == [128, 128]
+    assert F["moe_slot_to_row"].shape[0] == 16 + 8 + 16 + 8
+    for build in (om.build_indices_np, om.build_indices_py):
+        idx = build(m["ids"], m["gates"], m["e0"], m["n_local"])
+        for k in INDEX_KEYS:
+            assert np.array_equal(np.asarray(idx[k]), F["moe_" + k]), (build.__name__, k)
+    from mkernel_amd import ops  # the library's host C++ builder (no GPU call)
+    idx = ops.moe_build_indices(m["ids"], m["gates"], m["e0"], m["n_local"])
+    for k in INDEX_KEYS:
+        assert np.array_equal(idx[k], F["moe_" + k]), k
+
+
+def test_moe_layer_known_answer():
+    m = moe_inputs()
+    post = om.permute_ref(m["tokens"], F["moe_pull_indices"])
+    assert torch.equal(post, _bf(F["moe_post_x2"], 2))
+    _, ye = om.ffn_ref(post, m["w1"], m["w2"], F["moe_padded_tokens_per_expert"], m["I"])
+    assert torch.allclose(ye, torch.from_numpy(F["moe_y_expert"]), rtol=1e-5, atol=1e-5)
+    y = om.combine_ref(ye, F["moe_row_weight"], F["moe_pull_indices"], m["T"])
+    assert torch.allclose(y, torch.from_numpy(F["moe_y"]), rtol=1e-5, atol=1e-5)
+
+
+def test_moe_fixture_discriminates_silu_sign():
+    """The fixture's activations are large enough that silu with the sign of
+    its exponential flipped misses the expected output by far more than the
+    2e-2 parity tolerance (so a GPU path with that slip fails its test)."""
+    m = moe_inputs()
+    post = _bf(F["moe_post_x2"], 2)
+    h = om.grouped_gemm_ref(post, m["w1"], F["moe_padded_tokens_per_expert"])
+    g, u = h[:, :m["I"]], h[:, m["I"]:]
+    wrong = g / (1.0 + torch.exp(g)) * u
+    ye_wrong = torch.zeros_like(torch.from_numpy(F["moe_y_expert"]))
+    r = 0
+    for e, n in enumerate(F["moe_padded_tokens_per_expert"].tolist()):
+        ye_wrong[r:r + n] = wrong[r:r + n] @ m["w2"][e].float()
+        r += n
+    assert rel_fro(ye_wrong, torch.from_numpy(F["moe_y_expert"])) > 0.2
