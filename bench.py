@@ -230,6 +230,26 @@ def bench_moe(steps, warmup, extra):
     ids_d = torch.from_numpy(np.ascontiguousarray(ids_np, np.int32)).cuda()
     gates_d = torch.from_numpy(np.ascontiguousarray(gates_np, np.float32)).cuda()
     ms_idx = t.run(lambda i: ops.moe_build_indices_dev(ids_d, gates_d, cfg.e0, cfg.n_local, sync=False), steps, warmup)
+    # the routed layer from device top-k ids / gates with the row count left
+    # on the device (index build + FFN + combine, no host read-back), eager
+    # and replayed from a HIP graph recorded once
+    T_, k_ = ids_d.shape
+    cap = (T_ * k_ + cfg.n_local * 127 + 127) // 128 * 128
+    act_c = torch.empty((cap, cfg.I), dtype=torch.bfloat16, device="cuda")
+    ye_c = torch.empty((cap, cfg.H), dtype=torch.bfloat16, device="cuda")
+
+    def routed_layer(i=0):
+        tb = ops.moe_build_indices_dev(ids_d, gates_d, cfg.e0, cfg.n_local, sync=False)
+        ops.moe_ffn_combine(tokens, tb["pull_indices"], tb["row_weight"], tb["owner_offset"], tb["slot_to_row"], w1,
+                            w2, None, act_c, ye_c, y, rb_expert=tb["rb_expert"], rb_rows=tb["rb_rows"],
+                            fuse_dispatch=True, sizes=tb["sizes"])
+
+    routed_layer()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        routed_layer()
+    r_routed = interleaved({"eager": routed_layer, "graph": lambda i: graph.replay()}, steps, warmup)
     t0 = time.perf_counter()
     for _ in range(3):
         ops.moe_build_indices(ids_np, gates_np, cfg.e0, cfg.n_local)
@@ -255,6 +275,11 @@ def bench_moe(steps, warmup, extra):
                                 "weight_bytes": w_bytes1 + w_bytes2}
     extra["moe_index_build"] = {"us_gpu": ms_idx * 1e3, "us_host_cpp_1thread": ms_idx_host * 1e3,
                                 "entries": cfg.tokens * cfg.topk}
+    extra["moe_routed_layer_device_count"] = {
+        "what": "GPU index build + fused-dispatch FFN + combine from device top-k ids/gates, row count kept on the "
+                "device (buffers at capacity, no host read-back)",
+        "us_eager": r_routed["eager"] * 1e3, "us_graph_replay": r_routed["graph"] * 1e3,
+        "tokens_per_s_graph": cfg.tokens / r_routed["graph"] * 1e3, "capacity_rows": cap}
 
 
 # ------------------------------------------------------------ CPU baseline

@@ -246,6 +246,13 @@ typedef struct mk_moe_permute_args {
   int64_t R_pad, H;
   int64_t n_src_rows;
   int32_t tokens_per_src, devs_per_node;
+  /* Optional device row count {R, R_pad} (the `sizes` pair that
+   * mk_moe_build_indices_dev writes), or NULL.  When set, R_pad above is the
+   * row capacity the tables and buffers were sized for, and rows at or past
+   * sizes[1] are skipped, so the call needs no host read-back of the routed
+   * row count (and can be recorded in a HIP graph).  No counterpart in the
+   * reference, whose row counts come from its host builders. */
+  const int64_t* sizes;
 } mk_moe_permute_args;
 int mk_moe_permute(const mk_moe_permute_args* args, void* stream);
 
@@ -283,6 +290,11 @@ typedef struct mk_moe_grouped_gemm_args {
   int64_t n_src_rows;
   int32_t tokens_per_src, devs_per_node;
   int32_t tile_n;              /* output tile width: 256, 512 (Nw % 512 == 0), or 0 = library choice */
+  /* Optional device {R, R_pad}, as in mk_moe_permute_args: row tiles at or
+   * past sizes[1] are not computed (R_pad is the capacity) and the tail
+   * round's K-split is planned on the device; the split then needs
+   * split_ws to hold mk_query_workspace_bytes() bytes, else it is off. */
+  const int64_t* sizes;
 } mk_moe_grouped_gemm_args;
 int mk_moe_grouped_gemm(const mk_moe_grouped_gemm_args* args, void* stream);
 
@@ -345,6 +357,11 @@ typedef struct mk_moe_ffn_args {
   int64_t split_ws_bytes;
   int32_t fuse_dispatch;       /* 1: GEMM1 gathers tokens itself, post_tokens is not written */
   int32_t tile_n;              /* grouped GEMM tile width, as in mk_moe_grouped_gemm_args */
+  /* Optional device {R, R_pad}, as in mk_moe_permute_args: with it the
+   * whole layer (permute, both grouped GEMMs, combine) runs from the device
+   * tables of mk_moe_build_indices_dev at their capacity, with no host
+   * read-back between the index build and the combine. */
+  const int64_t* sizes;
 } mk_moe_ffn_args;
 int mk_moe_ffn_combine(const mk_moe_ffn_args* args, void* stream);
 

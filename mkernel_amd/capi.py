@@ -94,7 +94,7 @@ class MoeIndexDevArgs(C.Structure):
 
 class MoePermuteArgs(C.Structure):
     _fields_ = [("tokens", vp), ("pull_indices", vp), ("post_tokens", vp), ("R_pad", i64), ("H", i64),
-                ("n_src_rows", i64), ("tokens_per_src", i32), ("devs_per_node", i32)]
+                ("n_src_rows", i64), ("tokens_per_src", i32), ("devs_per_node", i32), ("sizes", vp)]
 
 
 class MoeGroupedGemmArgs(C.Structure):
@@ -102,7 +102,7 @@ class MoeGroupedGemmArgs(C.Structure):
                 ("rb_rows", vp), ("R_pad", i64), ("K", i64),
                 ("Nw", i64), ("num_experts", i32), ("mode", i32), ("num_cus", i32), ("split_ws", vp),
                 ("split_ws_bytes", i64), ("gather_pull", vp), ("n_src_rows", i64), ("tokens_per_src", i32),
-                ("devs_per_node", i32), ("tile_n", i32)]
+                ("devs_per_node", i32), ("tile_n", i32), ("sizes", vp)]
 
 
 class MoeCombineArgs(C.Structure):
@@ -117,7 +117,8 @@ class MoeFfnArgs(C.Structure):
                 ("act", vp), ("y_expert", vp), ("y_out", vp), ("num_tokens", i64), ("n_src_rows", i64),
                 ("R_pad", i64), ("H", i64), ("I", i64), ("num_experts", i32), ("tokens_per_src", i32),
                 ("devs_per_node", i32), ("out_dtype", i32), ("num_cus", i32), ("split_ws", vp),
-                ("split_ws_bytes", i64), ("fuse_dispatch", i32), ("tile_n", i32)]
+                ("split_ws_bytes", i64), ("fuse_dispatch", i32), ("tile_n", i32),
+                ("sizes", vp)]
 
 
 _lib = None

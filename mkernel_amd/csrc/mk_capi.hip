@@ -139,7 +139,7 @@ extern "C" {
 
 const char* mk_last_error_string(void) { return g_err.c_str(); }
 
-int32_t mk_abi_version(void) { return 3; }
+int32_t mk_abi_version(void) { return 4; }
 
 int mk_probe_mfma_ceiling(int64_t iters, int32_t num_wg, float* sink, uint64_t* clocks, void* stream) {
   if (!sink || !clocks) return fail(MK_EINVAL, "mk_probe_mfma_ceiling: null argument");
@@ -487,7 +487,7 @@ int mk_moe_permute(const mk_moe_permute_args* a, void* stream) {
   if (int rc = device_info(&d)) return rc;
   mk::PermuteKParams p{static_cast<const uint16_t*>(a->tokens), a->pull_indices,
                        static_cast<uint16_t*>(a->post_tokens), a->R_pad, a->H, a->n_src_rows,
-                       a->tokens_per_src, a->devs_per_node};
+                       a->tokens_per_src, a->devs_per_node, a->sizes ? a->sizes + 1 : nullptr};
   hipError_t e = mk::launch_permute(p, static_cast<hipStream_t>(stream));
   return e == hipSuccess ? MK_OK : hip_fail(e, "mk_moe_permute launch");
 }
@@ -496,7 +496,8 @@ static int grouped_gemm_impl(const void* A, const void* W, void* out, const int3
                              const int32_t* expert_rows, const int32_t* rb_rows, int64_t R_pad, int64_t K,
                              int64_t Nw, int32_t E, int32_t mode, int32_t num_cus, void* split_ws,
                              int64_t split_ws_bytes, const int32_t* gather_pull, int64_t n_src_rows,
-                             int32_t tokens_per_src, int32_t devs_per_node, int32_t tile_n, hipStream_t stream) {
+                             int32_t tokens_per_src, int32_t devs_per_node, int32_t tile_n,
+                             const int64_t* sizes, hipStream_t stream) {
   if (tile_n != 0 && tile_n != 256 && tile_n != 512)
     return fail(MK_EINVAL, "mk_moe_grouped_gemm: tile_n must be 0, 256 or 512");
   if (tile_n == 512 && Nw % 512) return fail(MK_ESHAPE, "mk_moe_grouped_gemm: tile_n 512 needs Nw %% 512 == 0");
@@ -547,7 +548,7 @@ static int grouped_gemm_impl(const void* A, const void* W, void* out, const int3
   // spreading the tiles evenly over ceil(tiles / rounds) workgroups (a
   // multiple of 8, for the XCD remap) gives each of them more bandwidth:
   // config-5 GEMM2 (658 tiles) 244 -> 231 us on 224 instead of 256.
-  {
+  if (!sizes) {
     const int ntiles = p.tiles_m * p.tiles_n, R = ntiles % p.n_cons;
     if (num_cus <= 0 && R != 0 && 2 * R > p.n_cons) {
       const int rounds = (ntiles + p.n_cons - 1) / p.n_cons;
@@ -556,7 +557,20 @@ static int grouped_gemm_impl(const void* A, const void* W, void* out, const int3
     }
   }
   if (int rc = check_ws(split_ws, split_ws_bytes, "mk_moe_grouped_gemm")) return rc;
-  plan_split(p, 128, split_ws, split_ws_bytes, bn);
+  if (sizes) {
+    // Row count on the device: the kernel clamps its row tiles to it and
+    // plans the tail split itself, which may use up to one partial tile per
+    // consumer (and one flag word each).
+    p.rows_dev = sizes + 1;
+    if (split_ws && p.waves == 8 && (int64_t)p.n_cons * 4 <= kSplitFlagBytes &&
+        split_ws_bytes >= kSplitFlagBytes + (int64_t)p.n_cons * 128 * bn * 4) {
+      p.sk_dev = 1;
+      p.sk_flags = static_cast<uint32_t*>(split_ws);
+      p.sk_ws = reinterpret_cast<float*>(static_cast<char*>(split_ws) + kSplitFlagBytes);
+    }
+  } else {
+    plan_split(p, 128, split_ws, split_ws_bytes, bn);
+  }
   hipError_t e = mk::launch_gemm(p, 128, mode == 1 ? mk::kEpiSwiGLU : mk::kEpiStore, stream, bn);
   return e == hipSuccess ? MK_OK : hip_fail(e, "mk_moe_grouped_gemm launch");
 }
@@ -565,7 +579,8 @@ int mk_moe_grouped_gemm(const mk_moe_grouped_gemm_args* a, void* stream) {
   if (!a) return fail(MK_EINVAL, "mk_moe_grouped_gemm: null argument");
   return grouped_gemm_impl(a->A, a->W, a->out, a->rb_expert, a->padded_tokens_per_expert, a->rb_rows, a->R_pad, a->K, a->Nw, a->num_experts, a->mode,
                            a->num_cus, a->split_ws, a->split_ws_bytes, a->gather_pull, a->n_src_rows,
-                           a->tokens_per_src, a->devs_per_node, a->tile_n, static_cast<hipStream_t>(stream));
+                           a->tokens_per_src, a->devs_per_node, a->tile_n, a->sizes,
+                           static_cast<hipStream_t>(stream));
 }
 
 int mk_moe_combine(const mk_moe_combine_args* a, void* stream) {
@@ -636,20 +651,20 @@ int mk_moe_ffn_combine(const mk_moe_ffn_args* a, void* stream) {
     if (int rc = grouped_gemm_impl(a->tokens, a->w1, a->act, a->rb_expert, a->padded_tokens_per_expert, a->rb_rows,
                                    a->R_pad, a->H, 2 * a->I, a->num_experts, 1, a->num_cus, a->split_ws,
                                    a->split_ws_bytes, a->pull_indices, a->n_src_rows, a->tokens_per_src,
-                                   a->devs_per_node, a->tile_n, s))
+                                   a->devs_per_node, a->tile_n, a->sizes, s))
       return rc;
   } else {
     mk_moe_permute_args pa{a->tokens, a->pull_indices, a->post_tokens, a->R_pad, a->H,
-                           a->n_src_rows, a->tokens_per_src, a->devs_per_node};
+                           a->n_src_rows, a->tokens_per_src, a->devs_per_node, a->sizes};
     if (int rc = mk_moe_permute(&pa, stream)) return rc;
     if (int rc = grouped_gemm_impl(a->post_tokens, a->w1, a->act, a->rb_expert, a->padded_tokens_per_expert,
                                    a->rb_rows, a->R_pad, a->H, 2 * a->I, a->num_experts, 1, a->num_cus,
-                                   a->split_ws, a->split_ws_bytes, nullptr, 0, 0, 0, a->tile_n, s))
+                                   a->split_ws, a->split_ws_bytes, nullptr, 0, 0, 0, a->tile_n, a->sizes, s))
       return rc;
   }
   if (int rc = grouped_gemm_impl(a->act, a->w2, a->y_expert, a->rb_expert, a->padded_tokens_per_expert,
                                  a->rb_rows, a->R_pad, a->I, a->H, a->num_experts, 0, a->num_cus, a->split_ws,
-                                 a->split_ws_bytes, nullptr, 0, 0, 0, a->tile_n, s))
+                                 a->split_ws_bytes, nullptr, 0, 0, 0, a->tile_n, a->sizes, s))
     return rc;
   mk_moe_combine_args ca{a->y_expert, a->row_weight, a->owner_offset, a->slot_to_row, a->y_out,
                          a->num_tokens, a->H, a->out_dtype};

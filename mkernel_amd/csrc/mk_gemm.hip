@@ -604,7 +604,29 @@ __device__ __forceinline__ void compute_role(const GemmKParams& p, int cons_id, 
   const int wave = tid >> 6;
   const int wm = wave / C::WN;
   const int wn = wave % C::WN;
-  const int ntiles = p.tiles_m * p.tiles_n;
+  // Row tiles and tail split from the launch parameters, or from the device
+  // row count (tiles past it are not walked; the split follows the rule the
+  // host's plan uses: R = tiles % n_cons tail tiles, each split
+  // min(4, n_cons / R, K stages / 4) ways when that is at least 2).
+  int tiles_m = p.tiles_m, sk_split = p.sk_split, sk_full = p.sk_full;
+  if constexpr (C::BM == 128) {
+    if (p.rows_dev) {
+      const int64_t rows = *p.rows_dev;
+      tiles_m = __builtin_amdgcn_readfirstlane((int)min<int64_t>(p.tiles_m, max<int64_t>(rows, 0) / C::BM));
+      const int nt = tiles_m * p.tiles_n;
+      sk_split = 0;
+      sk_full = nt;
+      const int R = nt % p.n_cons;
+      if (p.sk_dev && R != 0) {
+        const int s = min(min(4, p.n_cons / R), (p.K / 32) / 4);
+        if (s >= 2) {
+          sk_split = s;
+          sk_full = nt - R;
+        }
+      }
+    }
+  }
+  const int ntiles = tiles_m * p.tiles_n;
   const int nk_all = p.K / C::BKD;
 
   // A operand read: row wm*WTM + ml (+32 i), 16-byte unit 2kk + g.
@@ -630,8 +652,8 @@ __device__ __forceinline__ void compute_role(const GemmKParams& p, int cons_id, 
   const uint32_t lds_base = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)smem;
   const uint32_t wave_u = __builtin_amdgcn_readfirstlane(wave);
 
-  const int full = (p.sk_split > 1) ? p.sk_full : ntiles;
-  const int n_tail_units = (ntiles - full) * (p.sk_split > 1 ? p.sk_split : 0);
+  const int full = (sk_split > 1) ? sk_full : ntiles;
+  const int n_tail_units = (ntiles - full) * (sk_split > 1 ? sk_split : 0);
   const int n_full_mine = (full > cons_id) ? (full - cons_id + p.n_cons - 1) / p.n_cons : 0;
 
   // One output tile (or one K range of it): accumulate A[rows] @ B[:, cols]
@@ -642,7 +664,7 @@ __device__ __forceinline__ void compute_role(const GemmKParams& p, int cons_id, 
   auto tile_body = [&](int t, bool permuted, int k0, int nk, f32x16 (&acc)[C::FM][C::FN], int& m0_out,
                        int& tn_out) __attribute__((always_inline)) {
     int tm, tn;
-    decode_grouped(t, p.tiles_m, p.tiles_n, p.group_m, tm, tn);
+    decode_grouped(t, tiles_m, p.tiles_n, p.group_m, tm, tn);
     if (permuted) tm = row_perm[tm];
     // Tile coordinates are wave-uniform; keep them scalar.
     tm = __builtin_amdgcn_readfirstlane(tm);
@@ -964,14 +986,14 @@ __device__ __forceinline__ void compute_role(const GemmKParams& p, int cons_id, 
     for (int w = n_full_mine; w < sp.n_rounds; ++w) alt_stage<C::NT>(p, cons_id, sp, w);
   if (cons_id >= n_tail_units) return;
   // The K-split unit: tail tile full + tail_idx (unpermuted), K part `part`.
-  const int tail_idx = cons_id / p.sk_split;
-  const int part = cons_id % p.sk_split;
-  const int k0 = part * nk_all / p.sk_split;
-  const int nk = (part + 1) * nk_all / p.sk_split - k0;
+  const int tail_idx = cons_id / sk_split;
+  const int part = cons_id % sk_split;
+  const int k0 = part * nk_all / sk_split;
+  const int nk = (part + 1) * nk_all / sk_split - k0;
   f32x16 acc[C::FM][C::FN];
   int m0, tn;
   tile_body(full + tail_idx, false, k0, nk, acc, m0, tn);
-  if (C::WM == 2 && p.sk_split == 2 && EPI != kEpiReduce) {
+  if (C::WM == 2 && sk_split == 2 && EPI != kEpiReduce) {
     // Two-way split: the parts swap half tiles.  Part q finalizes the rows
     // of the waves with wm == q (rows q*WTM .. q*WTM + WTM - 1): the other
     // waves write their fp32 partial to this part's slot, and after the
@@ -1003,7 +1025,7 @@ __device__ __forceinline__ void compute_role(const GemmKParams& p, int cons_id, 
   }
   if (part > 0) {
     // K-split contributor: publish the partial for part 0 of this tile.
-    const int slot = tail_idx * (p.sk_split - 1) + part - 1;
+    const int slot = tail_idx * (sk_split - 1) + part - 1;
     put_partial<C>(p.sk_ws + (int64_t)slot * (C::BM * C::BN), acc, tid);
     // write-through stores performed at agent scope, then a relaxed flag
     // (the protocol of copy_wt: no L2 write-back needed)
@@ -1015,16 +1037,16 @@ __device__ __forceinline__ void compute_role(const GemmKParams& p, int cons_id, 
   {
     // K-split owner: acquire every contributor's partial, fold in part
     // order, and clear the flags for the next launch on this workspace.
-    const int slot0 = tail_idx * (p.sk_split - 1);
+    const int slot0 = tail_idx * (sk_split - 1);
     if (tid == 0)
       // one flag at a time: the split unit's registers are at the limit
-      for (int q2 = 0; q2 < p.sk_split - 1; ++q2)
+      for (int q2 = 0; q2 < sk_split - 1; ++q2)
         wait_flags<1>([&](int) { return p.sk_flags + slot0 + q2; }, 1, 1u, p.spin_limit, p.err);
     __syncthreads();
-    for (int q2 = 0; q2 < p.sk_split - 1; ++q2)
+    for (int q2 = 0; q2 < sk_split - 1; ++q2)
       add_partial<C>(p.sk_ws + (int64_t)(slot0 + q2) * (C::BM * C::BN), acc, tid, smem);
     if (tid == 0)
-      for (int q2 = 0; q2 < p.sk_split - 1; ++q2)
+      for (int q2 = 0; q2 < sk_split - 1; ++q2)
         __hip_atomic_store(p.sk_flags + slot0 + q2, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
   store_tile<C, EPI>(p, acc, m0, tn, tid, smem);

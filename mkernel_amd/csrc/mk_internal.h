@@ -63,6 +63,13 @@ struct GemmKParams {
   float* sk_ws;
   uint32_t* sk_flags;
   int sk_full, sk_split;
+  // Device row count (128-row grouped GEMMs launched at a row capacity
+  // before the routed row count is known on the host): *rows_dev rows are
+  // real, tiles past them are not walked, and with sk_dev the tail round's
+  // K-split is planned on the device by the host's rule (sk_ws / sk_flags
+  // then hold n_cons partial tiles).
+  const int64_t* rows_dev;
+  int sk_dev;
   // flag protocol
   uint32_t epoch;
   uint32_t spin_limit;
@@ -77,6 +84,7 @@ struct PermuteKParams {
   uint16_t* post;
   int64_t R_pad, H, n_src_rows;
   int tokens_per_src, devs_per_node;
+  const int64_t* rows_dev;  // device row count (rows at or past it are skipped), or null
 };
 hipError_t launch_permute(const PermuteKParams& p, hipStream_t stream);
 

@@ -12,8 +12,10 @@
 namespace mk {
 
 // One workgroup per padded row; padding rows (src_node < 0) are zero-filled.
+// With a device row count, rows past it (capacity rows) are left untouched.
 __global__ __launch_bounds__(kThreads) void permute_kernel(PermuteKParams p) {
   const int64_t r = blockIdx.x;
+  if (p.rows_dev && r >= *p.rows_dev) return;
   const int* pr = p.pull + 3 * r;
   const int src_node = pr[0], src_dev = pr[1], src_tok = pr[2];
   const int64_t vec = p.H / 8;

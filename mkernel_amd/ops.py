@@ -164,14 +164,18 @@ def moe_build_indices_dev(topk_ids: torch.Tensor, gates: torch.Tensor, e0: int, 
     top-k ids (int32) and gates (float32) [T, k].  Tables are allocated at
     the worst-case capacity; with sync=True the sizes are read back and the
     returned tensors are views trimmed to R / R_pad rows (the same dict
-    layout as moe_build_indices, as device tensors)."""
+    layout as moe_build_indices, as device tensors).  With sync=False nothing
+    is read back: the tables stay at their capacity and "sizes" holds the
+    device int64 {R, R_pad} for moe_ffn_combine(..., sizes=...)."""
     if topk_ids.dtype != torch.int32 or gates.dtype != torch.float32 or not topk_ids.is_cuda:
         raise ValueError("topk_ids must be int32 and gates float32 device tensors")
     ids = topk_ids.contiguous()
     g = gates.contiguous()
     T, k = ids.shape
     dev = ids.device
-    cap = T * k + n_local * (row_block - 1)
+    # worst case, rounded to whole row blocks so the capacity is a valid
+    # row count for the grouped GEMMs
+    cap = (T * k + n_local * (row_block - 1) + row_block - 1) // row_block * row_block
     i32 = dict(dtype=torch.int32, device=dev)
     t = {
         "padded_tokens_per_expert": torch.empty(n_local, **i32),
@@ -206,20 +210,24 @@ def moe_build_indices_dev(topk_ids: torch.Tensor, gates: torch.Tensor, e0: int, 
     return t
 
 
-def moe_permute(tokens, pull, post, tokens_per_src: int | None = None, devs_per_node: int = 1):
+def moe_permute(tokens, pull, post, tokens_per_src: int | None = None, devs_per_node: int = 1, sizes=None):
+    """sizes: optional device int64 {R, R_pad}; post's rows are then a
+    capacity and rows past R_pad are skipped."""
     _bf16(tokens, "tokens"); _bf16(post, "post_tokens")
     R_pad, H = post.shape
     tps = tokens.shape[0] if tokens_per_src is None else tokens_per_src
     capi.call("mk_moe_permute", MoePermuteArgs(_ptr(tokens), _ptr(pull), _ptr(post), R_pad, H, tokens.shape[0], tps,
-                                                devs_per_node), _stream())
+                                                devs_per_node, _ptr(sizes)), _stream())
     return post
 
 
 def moe_grouped_gemm(A, W, out, rb_expert=None, padded_tokens_per_expert=None, mode: int = 0, num_cus: int = 0,
                      rb_rows=None, split_ws=None, gather_pull=None, tokens_per_src: int | None = None,
-                     devs_per_node: int = 1, tile_n: int = 0):
+                     devs_per_node: int = 1, tile_n: int = 0, sizes=None):
     """mode 0: out = A @ W[e]; mode 1: out = silu(h[:, :I]) * h[:, I:], h = A @ W[e].
-    tile_n: output tile width 256 or 512 (0: the library's choice)."""
+    tile_n: output tile width 256 or 512 (0: the library's choice).  sizes:
+    optional device int64 {R, R_pad}; the row count is then a capacity and
+    row tiles past R_pad are not computed."""
     _bf16(A, "A"); _bf16(W, "W"); _bf16(out, "out")
     # with gather_pull, A is the token buffer and the rows come from the pull table
     R_pad = gather_pull.shape[0] if gather_pull is not None else A.shape[0]
@@ -228,7 +236,7 @@ def moe_grouped_gemm(A, W, out, rb_expert=None, padded_tokens_per_expert=None, m
     tps = A.shape[0] if tokens_per_src is None else tokens_per_src
     args = MoeGroupedGemmArgs(_ptr(A), _ptr(W), _ptr(out), _ptr(rb_expert), _ptr(padded_tokens_per_expert),
                               _ptr(rb_rows), R_pad, K, Nw, E, mode, num_cus, *_ws(split_ws, A.device),
-                              _ptr(gather_pull), A.shape[0], tps, devs_per_node, tile_n)
+                              _ptr(gather_pull), A.shape[0], tps, devs_per_node, tile_n, _ptr(sizes))
     capi.call("mk_moe_grouped_gemm", args, _stream())
     return out
 
@@ -260,10 +268,13 @@ def moe_combine(y_expert, row_weight, owner_offset, slot_to_row, y_out):
 def moe_ffn_combine(tokens, pull, row_weight, owner_offset, slot_to_row, w1, w2, post, act, y_expert, y_out,
                     rb_expert=None, padded_tokens_per_expert=None, tokens_per_src: int | None = None,
                     devs_per_node: int = 1, num_cus: int = 0, rb_rows=None, split_ws=None,
-                    fuse_dispatch: bool = False, tile_n: int = 0):
+                    fuse_dispatch: bool = False, tile_n: int = 0, sizes=None):
     """permute -> grouped GEMM1 + SwiGLU -> grouped GEMM2 -> combine.  With
     fuse_dispatch, GEMM1 reads the token rows through the pull table itself
-    (no permute kernel, post may be None and is not written)."""
+    (no permute kernel, post may be None and is not written).  sizes: the
+    device {R, R_pad} of moe_build_indices_dev(sync=False); the tables and
+    buffers are then at their capacity and nothing is read back to the host
+    (the call can be recorded in a CUDA/HIP graph)."""
     T, H = y_out.shape
     E, _, I2 = w1.shape
     R_pad = pull.shape[0]
@@ -273,7 +284,7 @@ def moe_ffn_combine(tokens, pull, row_weight, owner_offset, slot_to_row, w1, w2,
                       _ptr(row_weight),
                       _ptr(owner_offset), _ptr(slot_to_row), _ptr(w1), _ptr(w2), _ptr(post), _ptr(act), _ptr(y_expert),
                       _ptr(y_out), T, tokens.shape[0], R_pad, H, I2 // 2, E, tps, devs_per_node, od, num_cus,
-                      *_ws(split_ws, tokens.device), int(fuse_dispatch), tile_n)
+                      *_ws(split_ws, tokens.device), int(fuse_dispatch), tile_n, _ptr(sizes))
     capi.call("mk_moe_ffn_combine", args, _stream())
     return y_out
 

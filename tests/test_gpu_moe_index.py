@@ -94,3 +94,109 @@ def test_index_dev_feeds_ffn(dev):
                             w1.to(dev), w2.to(dev), post, act, ye, y, rb_expert=d["rb_expert"], rb_rows=d["rb_rows"])
         outs.append(y.cpu())
     assert torch.equal(outs[0], outs[1])
+
+
+# --- the routed layer with the row count left on the device -----------------
+
+LAYER = wl.MoeCfg(tokens=512, H=512, I=256, experts=64, topk=8, ep=8, rank=0)
+
+
+def _host_layer(dev, cfg, tokens, w1, w2, ids, gates, split_ws, fuse):
+    """Reference run: host-built tables, host R_pad."""
+    h = ops.moe_build_indices(ids, gates, cfg.e0, cfg.n_local)
+    d = {k: torch.from_numpy(np.ascontiguousarray(v)).to(dev) for k, v in h.items() if isinstance(v, np.ndarray)}
+    Rp = h["R_pad"]
+    post = torch.empty((Rp, cfg.H), dtype=torch.bfloat16, device=dev)
+    act = torch.empty((Rp, cfg.I), dtype=torch.bfloat16, device=dev)
+    ye = torch.empty((Rp, cfg.H), dtype=torch.bfloat16, device=dev)
+    y = torch.empty((cfg.tokens, cfg.H), dtype=torch.bfloat16, device=dev)
+    ops.moe_ffn_combine(tokens, d["pull_indices"], d["row_weight"], d["owner_offset"], d["slot_to_row"], w1, w2, post,
+                        act, ye, y, rb_expert=d["rb_expert"], rb_rows=d["rb_rows"], split_ws=split_ws,
+                        fuse_dispatch=fuse)
+    return y
+
+
+class _DeviceLayer:
+    """Index build + FFN + combine with every buffer at the row capacity and
+    the row count only on the device (nothing read back)."""
+
+    def __init__(self, dev, cfg, tokens, w1, w2, ids_d, gates_d, split_ws, fuse):
+        self.cfg, self.tokens, self.w1, self.w2, self.ids, self.gates = cfg, tokens, w1, w2, ids_d, gates_d
+        self.split_ws, self.fuse = split_ws, fuse
+        T, k = ids_d.shape
+        cap = (T * k + cfg.n_local * 127 + 127) // 128 * 128
+        self.post = torch.empty((cap, cfg.H), dtype=torch.bfloat16, device=dev)
+        self.act = torch.empty((cap, cfg.I), dtype=torch.bfloat16, device=dev)
+        self.ye = torch.empty((cap, cfg.H), dtype=torch.bfloat16, device=dev)
+        self.y = torch.empty((cfg.tokens, cfg.H), dtype=torch.bfloat16, device=dev)
+
+    def __call__(self):
+        c = self.cfg
+        t = ops.moe_build_indices_dev(self.ids, self.gates, c.e0, c.n_local, sync=False)
+        assert t["pull_indices"].shape[0] == self.post.shape[0]
+        ops.moe_ffn_combine(self.tokens, t["pull_indices"], t["row_weight"], t["owner_offset"], t["slot_to_row"],
+                            self.w1, self.w2, self.post, self.act, self.ye, self.y, rb_expert=t["rb_expert"],
+                            rb_rows=t["rb_rows"], split_ws=self.split_ws, fuse_dispatch=self.fuse, sizes=t["sizes"])
+        return self.y
+
+
+def _routing(cfg, seed):
+    ids, gates = wl.zipf_routing(cfg.tokens, cfg.experts, cfg.topk, cfg.zipf_s, seed)
+    return np.ascontiguousarray(ids, np.int32), np.ascontiguousarray(gates, np.float32)
+
+
+@pytest.mark.parametrize("fuse", [False, True])
+def test_layer_with_device_row_count(dev, fuse):
+    """Without the K-split every output tile is one workgroup's full-K sum,
+    so the capacity-sized launch gives the host-sized launch's bits; with the
+    split (planned on the device) it stays within the parity bound."""
+    _say(f"moe layer, device row count, fuse={fuse}")
+    from oracle.gemm import rel_fro
+    cfg = LAYER
+    tokens, _, _, w1, w2 = wl.moe_inputs(cfg)
+    tokens, w1, w2 = tokens.to(dev), w1.to(dev), w2.to(dev)
+    ids, gates = _routing(cfg, 6)
+    ids_d, gates_d = torch.from_numpy(ids).to(dev), torch.from_numpy(gates).to(dev)
+    ref = _host_layer(dev, cfg, tokens, w1, w2, ids, gates, False, fuse).cpu()
+    y = _DeviceLayer(dev, cfg, tokens, w1, w2, ids_d, gates_d, False, fuse)().cpu()
+    assert torch.equal(y, ref)
+    y_split = _DeviceLayer(dev, cfg, tokens, w1, w2, ids_d, gates_d, None, fuse)().cpu()
+    assert rel_fro(y_split.float(), ref.float()) < 1e-2
+    # no routed rows at all: R_pad = 0 on the device, every output row zero
+    none_d = torch.full_like(ids_d, cfg.experts - 1)
+    y0 = _DeviceLayer(dev, cfg, tokens, w1, w2, none_d, gates_d, None, fuse)().cpu()
+    assert (y0 == 0).all()
+
+
+@pytest.mark.parametrize("split", [False, None])
+def test_layer_graph_replays(dev, split):
+    """The whole routed layer recorded once in a HIP graph and replayed with
+    new routings written into the captured inputs; every replay matches an
+    eager run on the same routing (bit-exact), with eager library work and
+    synchronizations between the replays."""
+    _say(f"moe layer graph replays split={split}")
+    cfg = LAYER
+    tokens, _, _, w1, w2 = wl.moe_inputs(cfg)
+    tokens, w1, w2 = tokens.to(dev), w1.to(dev), w2.to(dev)
+    ids0, gates0 = _routing(cfg, 6)
+    ids_d, gates_d = torch.from_numpy(ids0).to(dev), torch.from_numpy(gates0).to(dev)
+    layer = _DeviceLayer(dev, cfg, tokens, w1, w2, ids_d, gates_d, split, False)
+    eager = {}
+    for seed in (6, 7, 8):
+        ids, gates = _routing(cfg, seed)
+        ids_d.copy_(torch.from_numpy(ids)); gates_d.copy_(torch.from_numpy(gates))
+        eager[seed] = layer().clone()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        layer()
+    for seed in (7, 6, 8, 7):
+        ids, gates = _routing(cfg, seed)
+        ids_d.copy_(torch.from_numpy(ids)); gates_d.copy_(torch.from_numpy(gates))
+        layer.y.fill_(-1.0)
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(layer.y, eager[seed]), seed
+        # eager library work between replays
+        ops.gemm(tokens[:256], w1[0, :, :256].contiguous())
+        torch.cuda.synchronize()
