@@ -230,6 +230,12 @@ def bench_moe(steps, warmup, extra):
     ids_d = torch.from_numpy(np.ascontiguousarray(ids_np, np.int32)).cuda()
     gates_d = torch.from_numpy(np.ascontiguousarray(gates_np, np.float32)).cuda()
     ms_idx = t.run(lambda i: ops.moe_build_indices_dev(ids_d, gates_d, cfg.e0, cfg.n_local, sync=False), steps, warmup)
+    # the host C++ builder (one thread) for comparison
+    ops.moe_build_indices(ids_np, gates_np, cfg.e0, cfg.n_local)
+    t0 = time.perf_counter()
+    for _ in range(3):
+        ops.moe_build_indices(ids_np, gates_np, cfg.e0, cfg.n_local)
+    ms_idx_host = (time.perf_counter() - t0) / 3 * 1e3
     # the routed layer from device top-k ids / gates with the row count left
     # on the device (index build + FFN + combine, no host read-back), eager
     # and replayed from a HIP graph recorded once
@@ -250,10 +256,6 @@ def bench_moe(steps, warmup, extra):
     with torch.cuda.graph(graph):
         routed_layer()
     r_routed = interleaved({"eager": routed_layer, "graph": lambda i: graph.replay()}, steps, warmup)
-    t0 = time.perf_counter()
-    for _ in range(3):
-        ops.moe_build_indices(ids_np, gates_np, cfg.e0, cfg.n_local)
-    ms_idx_host = (time.perf_counter() - t0) / 3 * 1e3
     used = idx["padded_tokens_per_expert"] > 0
     w_bytes1 = int(used.sum()) * cfg.H * 2 * cfg.I * 2
     w_bytes2 = int(used.sum()) * cfg.I * cfg.H * 2
