@@ -100,6 +100,11 @@ typedef struct mk_ag_gemm_args {
                               zero-filled before its first use, left zeroed by every
                               launch; NULL = no K-split of the tail round */
   int64_t split_ws_bytes;
+  /* Optional device word holding the epoch: when set, the launch reads the
+   * epoch from it (never 0) instead of `epoch`, so a HIP graph that records
+   * mk_epoch_advance and this launch gates every replay on a new epoch with
+   * no host work.  NULL = use `epoch`. */
+  const uint32_t* epoch_ptr;
 } mk_ag_gemm_args;
 int mk_ag_gemm(const mk_ag_gemm_args* args, void* stream);
 
@@ -136,6 +141,11 @@ typedef struct mk_gemm_rs_args {
                               zero-filled before its first use, left zeroed by every
                               launch; NULL = no K-split of the tail round */
   int64_t split_ws_bytes;
+  /* Optional device word holding the epoch: when set, the launch reads the
+   * epoch from it (never 0) instead of `epoch`, so a HIP graph that records
+   * mk_epoch_advance and this launch gates every replay on a new epoch with
+   * no host work.  NULL = use `epoch`. */
+  const uint32_t* epoch_ptr;
 } mk_gemm_rs_args;
 int mk_gemm_rs(const mk_gemm_rs_args* args, void* stream);
 
@@ -174,6 +184,11 @@ typedef struct mk_gemm_ar_args {
   uint32_t* done_flags;         /* [(M/256) * (N/256)] or NULL */
   void* split_ws;
   int64_t split_ws_bytes;
+  /* Optional device word holding the epoch: when set, the launch reads the
+   * epoch from it (never 0) instead of `epoch`, so a HIP graph that records
+   * mk_epoch_advance and this launch gates every replay on a new epoch with
+   * no host work.  NULL = use `epoch`. */
+  const uint32_t* epoch_ptr;
 } mk_gemm_ar_args;
 int mk_gemm_ar(const mk_gemm_ar_args* args, void* stream);
 
@@ -395,7 +410,15 @@ int32_t mk_device_cu_count(void);
 
 const char* mk_last_error_string(void);
 
-/* ABI version, bumped on any signature change (2: split_ws fields). */
+/* Advances a device epoch word on the stream: *epoch_ptr += 1, skipping 0
+ * (the value flags start at).  Recorded in a HIP graph before gated launches
+ * that read epoch_ptr, it gives each replay a new epoch.  Device-side
+ * counterpart of the reference's host epoch helpers (set_epoch /
+ * prepare_epoch / commit_epoch, include/operators/ag_gemm/session.cuh:192-230). */
+int mk_epoch_advance(uint32_t* epoch_ptr, void* stream);
+
+/* ABI version, bumped on any signature change (2: split_ws fields; 4: MoE
+ * `sizes`; 5: epoch_ptr). */
 int32_t mk_abi_version(void);
 
 #ifdef __cplusplus

@@ -35,6 +35,7 @@ EXPORTS = (
     "mk_device_cu_count",
     "mk_last_error_string",
     "mk_abi_version",
+    "mk_epoch_advance",
 )
 
 vp = C.c_void_p
@@ -62,7 +63,7 @@ class AgGemmArgs(C.Structure):
                 ("M", i64), ("N", i64), ("K", i64),
                 ("flags", vp), ("stage_order", vp), ("epoch", u32), ("gated", i32),
                 ("num_producers", i32), ("num_cus", i32), ("spin_limit", u32), ("error_word", vp),
-                ("stage_counters", vp), ("split_ws", vp), ("split_ws_bytes", i64)]
+                ("stage_counters", vp), ("split_ws", vp), ("split_ws_bytes", i64), ("epoch_ptr", vp)]
 
 
 class GemmRsArgs(C.Structure):
@@ -70,14 +71,15 @@ class GemmRsArgs(C.Structure):
                 ("peer_recv", vp), ("M", i64), ("N", i64), ("K", i64), ("world", i32), ("rank", i32),
                 ("flags", vp), ("stage_order", vp), ("epoch", u32), ("gated", i32),
                 ("num_producers", i32), ("num_cus", i32), ("spin_limit", u32), ("error_word", vp),
-                ("stage_counters", vp), ("split_ws", vp), ("split_ws_bytes", i64)]
+                ("stage_counters", vp), ("split_ws", vp), ("split_ws_bytes", i64), ("epoch_ptr", vp)]
 
 
 class GemmArArgs(C.Structure):
     _fields_ = [("A", vp), ("B", vp), ("C_final", vp), ("peer_src", vp), ("peer_recv", vp), ("M", i64), ("N", i64),
                 ("K", i64), ("world", i32), ("flags", vp), ("stage_order", vp), ("epoch", u32), ("gated", i32),
                 ("num_producers", i32), ("num_cus", i32), ("spin_limit", u32), ("error_word", vp),
-                ("stage_counters", vp), ("done_flags", vp), ("split_ws", vp), ("split_ws_bytes", i64)]
+                ("stage_counters", vp), ("done_flags", vp), ("split_ws", vp), ("split_ws_bytes", i64),
+                ("epoch_ptr", vp)]
 
 
 class MoeIndex(C.Structure):
@@ -158,6 +160,8 @@ def lib() -> C.CDLL:
         L.mk_device_cu_count.restype = i32
         L.mk_last_error_string.argtypes = []
         L.mk_last_error_string.restype = C.c_char_p
+        L.mk_epoch_advance.argtypes = [vp, vp]
+        L.mk_epoch_advance.restype = i32
         L.mk_abi_version.argtypes = []
         L.mk_abi_version.restype = i32
         _lib = L

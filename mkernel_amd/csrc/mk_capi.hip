@@ -139,7 +139,15 @@ extern "C" {
 
 const char* mk_last_error_string(void) { return g_err.c_str(); }
 
-int32_t mk_abi_version(void) { return 4; }
+int32_t mk_abi_version(void) { return 5; }
+
+int mk_epoch_advance(uint32_t* epoch_ptr, void* stream) {
+  if (!epoch_ptr) return fail(MK_EINVAL, "mk_epoch_advance: null argument");
+  DevInfo d;
+  if (int rc = device_info(&d)) return rc;
+  hipError_t e = mk::launch_epoch_advance(epoch_ptr, static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? MK_OK : hip_fail(e, "mk_epoch_advance launch");
+}
 
 int mk_probe_mfma_ceiling(int64_t iters, int32_t num_wg, float* sink, uint64_t* clocks, void* stream) {
   if (!sink || !clocks) return fail(MK_EINVAL, "mk_probe_mfma_ceiling: null argument");
@@ -208,7 +216,7 @@ int mk_ag_gemm(const mk_ag_gemm_args* a, void* stream) {
   const int64_t nflags = a->M / 128;
   if (a->gated) {
     if (!a->flags) return fail(MK_EINVAL, "mk_ag_gemm: gated launch needs flags");
-    if (a->epoch == 0) return fail(MK_EINVAL, "mk_ag_gemm: epoch 0 is reserved (flags start at 0)");
+    if (a->epoch == 0 && !a->epoch_ptr) return fail(MK_EINVAL, "mk_ag_gemm: epoch 0 is reserved (flags start at 0)");
     if (a->stage_order && a->M / bm > mk::kMaxTilesM)
       return fail(MK_ESHAPE, "mk_ag_gemm: arrival-ordered schedule supports at most %d row tiles", mk::kMaxTilesM);
     if (nflags + a->M / bm > 8192)
@@ -233,6 +241,7 @@ int mk_ag_gemm(const mk_ag_gemm_args* a, void* stream) {
   p.tiles_n = (int)(a->N / 256);
   set_grid(p, total, n_prod, p.tiles_m * p.tiles_n);
   p.epoch = a->epoch;
+  p.epoch_ptr = a->epoch_ptr;
   p.spin_limit = a->spin_limit;
   p.err = a->error_word;
   if (a->gated) {
@@ -276,7 +285,7 @@ int mk_gemm_rs(const mk_gemm_rs_args* a, void* stream) {
   const int n_prod = (a->gated && npeers > 0 && a->num_producers > 0) ? a->num_producers : 0;
   if (a->gated && npeers > 0) {
     if (!a->flags) return fail(MK_EINVAL, "mk_gemm_rs: gated launch needs flags");
-    if (a->epoch == 0) return fail(MK_EINVAL, "mk_gemm_rs: epoch 0 is reserved");
+    if (a->epoch == 0 && !a->epoch_ptr) return fail(MK_EINVAL, "mk_gemm_rs: epoch 0 is reserved");
     if (a->num_producers != 0 && !a->peer_src) return fail(MK_EINVAL, "mk_gemm_rs: staging needs peer_src");
     if (coop && !a->stage_counters) return fail(MK_EINVAL, "mk_gemm_rs: cooperative staging needs stage_counters");
   }
@@ -298,6 +307,7 @@ int mk_gemm_rs(const mk_gemm_rs_args* a, void* stream) {
   p.rs_recv = static_cast<const uint16_t*>(a->peer_recv);
   p.rs_out = static_cast<uint16_t*>(a->output);
   p.epoch = a->epoch;
+  p.epoch_ptr = a->epoch_ptr;
   p.spin_limit = a->spin_limit;
   p.err = a->error_word;
   if (a->gated && npeers > 0) {
@@ -343,7 +353,8 @@ int mk_gemm_ar(const mk_gemm_ar_args* a, void* stream) {
     if (a->num_producers != 0 && !a->peer_src) return fail(MK_EINVAL, "mk_gemm_ar: staging needs peer_src");
     if (coop && !a->stage_counters) return fail(MK_EINVAL, "mk_gemm_ar: cooperative staging needs stage_counters");
   }
-  if ((gated || a->done_flags) && a->epoch == 0) return fail(MK_EINVAL, "mk_gemm_ar: epoch 0 is reserved");
+  if ((gated || a->done_flags) && a->epoch == 0 && !a->epoch_ptr)
+    return fail(MK_EINVAL, "mk_gemm_ar: epoch 0 is reserved");
   if (n_prod >= total) return fail(MK_EINVAL, "mk_gemm_ar: bad num_producers");
   mk::GemmKParams p;
   fill_common(p);
@@ -362,6 +373,7 @@ int mk_gemm_ar(const mk_gemm_ar_args* a, void* stream) {
   p.rs_out = static_cast<uint16_t*>(a->C_final);
   p.ar_done = a->done_flags;
   p.epoch = a->epoch;
+  p.epoch_ptr = a->epoch_ptr;
   p.spin_limit = a->spin_limit;
   p.err = a->error_word;
   if (gated) {

@@ -112,6 +112,15 @@ __device__ __forceinline__ int b_block(int wn, int jb) {
   }
 }
 
+// Epoch of this launch: the device word when the caller passed one (it was
+// written by an earlier launch on the stream, so it is visible and fixed for
+// the whole launch), else the launch argument.
+__device__ __forceinline__ uint32_t launch_epoch(const GemmKParams& p) {
+  return p.epoch_ptr
+             ? __builtin_amdgcn_readfirstlane(__hip_atomic_load(p.epoch_ptr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))
+             : p.epoch;
+}
+
 // ---------------------------------------------------------------------------
 // Producer role: copy 128-row blocks src -> dst in stage order, then publish.
 // ---------------------------------------------------------------------------
@@ -124,7 +133,7 @@ __device__ void producer_role(const GemmKParams& p, int pid) {
     // every wave's write-through stores performed, then one publication
     wait_vmem_all();
     __syncthreads();
-    if (threadIdx.x == 0) __hip_atomic_store(p.st_flags + b, p.epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (threadIdx.x == 0) __hip_atomic_store(p.st_flags + b, launch_epoch(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }
 
@@ -157,7 +166,7 @@ __device__ void coop_stage(const GemmKParams& p, int stride, int& q, int& batch,
   auto count_piece = [&](int b) {
     const uint32_t old = __hip_atomic_fetch_add(p.st_counters + b, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (old % kPieces == kPieces - 1)
-      __hip_atomic_store(p.st_flags + b, p.epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(p.st_flags + b, launch_epoch(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   };
   // Pieces are counted in batches of p.st_batch: copy the batch, wait for
   // the stores, one barrier, then count the batch's pieces; the first batch
@@ -340,7 +349,7 @@ __device__ __forceinline__ void store_tile(const GemmKParams& p, f32x16 (&acc)[C
         constexpr int per = C::BM / kFlagRows;
         if (tid == 0)
           wait_flags<16>([&](int f) { return p.rs_flags + (f / per) * rbs + lr0 / kFlagRows + f % per; },
-                     p.rs_npeers * per, p.epoch, p.spin_limit, p.err);
+                     p.rs_npeers * per, launch_epoch(p), p.spin_limit, p.err);
         __syncthreads();
       }
       reduce_rows<C>(p, acc, lr0 + wm * C::WTM, tn * C::BN + wn * C::WTN, smem, wave, lane);
@@ -349,7 +358,7 @@ __device__ __forceinline__ void store_tile(const GemmKParams& p, f32x16 (&acc)[C
         // all-reduce: publish the finished tile (the broadcast hand-off).
         // The tile's rows are plain stores, so the flag is a release store:
         // one L2 write-back per tile.
-        if (tid == 0) publish_flag(p.ar_done + (m0 / C::BM) * p.tiles_n + tn, p.epoch);
+        if (tid == 0) publish_flag(p.ar_done + (m0 / C::BM) * p.tiles_n + tn, launch_epoch(p));
       }
     }
   }
@@ -700,7 +709,7 @@ __device__ __forceinline__ void compute_role(const GemmKParams& p, int cons_id, 
     // Flag gate on the A rows of this tile (AllGather consumer side).
     if (p.a_flags) {
       if (tid == 0)
-        wait_flags<C::BM / kFlagRows>([&](int f) { return p.a_flags + m0 / kFlagRows + f; }, C::BM / kFlagRows, p.epoch, p.spin_limit,
+        wait_flags<C::BM / kFlagRows>([&](int f) { return p.a_flags + m0 / kFlagRows + f; }, C::BM / kFlagRows, launch_epoch(p), p.spin_limit,
                    p.err);
       __syncthreads();
     }
@@ -1216,6 +1225,21 @@ __global__ __launch_bounds__(64 * WAVES, 1) void gemm_kernel(GemmKParams p) {
     }
   }
   compute_role<C, EPI>(p, cons, smem, perm, flist, sp);
+}
+
+// One thread: *epoch_ptr + 1, skipping 0 (a vector store, ordered before
+// the next launch on the stream by the kernel boundary).
+__global__ void epoch_advance_kernel(uint32_t* epoch_ptr) {
+  if (threadIdx.x == 0) {
+    uint32_t e = __hip_atomic_load(epoch_ptr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
+    if (e == 0u) e = 1u;
+    __hip_atomic_store(epoch_ptr, e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
+hipError_t launch_epoch_advance(uint32_t* epoch_ptr, hipStream_t stream) {
+  hipLaunchKernelGGL(epoch_advance_kernel, dim3(1), dim3(64), 0, stream, epoch_ptr);
+  return hipGetLastError();
 }
 
 // ---------------------------------------------------------------------------

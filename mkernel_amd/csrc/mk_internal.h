@@ -70,13 +70,16 @@ struct GemmKParams {
   // then hold n_cons partial tiles).
   const int64_t* rows_dev;
   int sk_dev;
-  // flag protocol
+  // flag protocol: the epoch is *epoch_ptr when that is set (read once per
+  // use at run time, written by an earlier launch), else `epoch`
+  const uint32_t* epoch_ptr;
   uint32_t epoch;
   uint32_t spin_limit;
   uint32_t* err;
 };
 
 hipError_t launch_gemm(const GemmKParams& p, int bm, int epi, hipStream_t stream, int bn = 256);
+hipError_t launch_epoch_advance(uint32_t* epoch_ptr, hipStream_t stream);
 
 struct PermuteKParams {
   const uint16_t* tokens;

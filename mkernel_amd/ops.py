@@ -78,8 +78,10 @@ def gemm(A: torch.Tensor, B: torch.Tensor, out: torch.Tensor | None = None, num_
 
 def ag_gemm(A_shards, A_full, B, C_out, flags, stage_order, epoch: int, gated: bool = True,
             num_producers: int = -1, num_cus: int = 0, spin_limit: int = 0, error_word=None,
-            stage_counters=None, split_ws=None) -> torch.Tensor:
-    """Flag-gated AllGather+GEMM; see include/mk.h mk_ag_gemm.  num_producers
+            stage_counters=None, split_ws=None, epoch_ptr=None) -> torch.Tensor:
+    """Flag-gated AllGather+GEMM; see include/mk.h mk_ag_gemm.  epoch_ptr: an
+    optional uint32 device word read for the epoch instead of `epoch`
+    (advanced by epoch_advance, e.g. inside a recorded graph).  num_producers
     -1 (default) stages cooperatively, the two halves of the grid taking
     turns to copy ahead; -2 stages cooperatively with every workgroup copying
     an even share before every round.  Both need stage_counters (int32
@@ -89,28 +91,29 @@ def ag_gemm(A_shards, A_full, B, C_out, flags, stage_order, epoch: int, gated: b
     N = B.shape[1]
     args = AgGemmArgs(_ptr(A_shards), _ptr(A_full), _ptr(B), _ptr(C_out), M, N, K, _ptr(flags), _ptr(stage_order),
                       epoch, int(gated), num_producers, num_cus, spin_limit, _ptr(error_word), _ptr(stage_counters),
-                      *_ws(split_ws, A_full.device))
+                      *_ws(split_ws, A_full.device), _ptr(epoch_ptr))
     capi.call("mk_ag_gemm", args, _stream())
     return C_out
 
 
 def gemm_rs(A, B, workspace, output, peer_src, peer_recv, world: int, rank: int, flags, stage_order, epoch: int,
             gated: bool = True, num_producers: int = -1, num_cus: int = 0, spin_limit: int = 0,
-            error_word=None, stage_counters=None, split_ws=None) -> torch.Tensor:
-    """GEMM with the reduce-scatter fold in the epilogue; see mk_gemm_rs."""
+            error_word=None, stage_counters=None, split_ws=None, epoch_ptr=None) -> torch.Tensor:
+    """GEMM with the reduce-scatter fold in the epilogue; see mk_gemm_rs.
+    epoch_ptr: as in ag_gemm."""
     _bf16(A, "A"); _bf16(B, "B")
     M, K = A.shape
     N = B.shape[1]
     args = GemmRsArgs(_ptr(A), _ptr(B), _ptr(workspace), _ptr(output), _ptr(peer_src), _ptr(peer_recv), M, N, K,
                       world, rank, _ptr(flags), _ptr(stage_order), epoch, int(gated), num_producers, num_cus,
-                      spin_limit, _ptr(error_word), _ptr(stage_counters), *_ws(split_ws, A.device))
+                      spin_limit, _ptr(error_word), _ptr(stage_counters), *_ws(split_ws, A.device), _ptr(epoch_ptr))
     capi.call("mk_gemm_rs", args, _stream())
     return output
 
 
 def gemm_ar(A, B, C_final, peer_src, peer_recv, world: int, flags, stage_order, epoch: int, gated: bool = True,
             num_producers: int = -1, num_cus: int = 0, spin_limit: int = 0, error_word=None, stage_counters=None,
-            done_flags=None, split_ws=None) -> torch.Tensor:
+            done_flags=None, split_ws=None, epoch_ptr=None) -> torch.Tensor:
     """GEMM + all-reduce at one rank's share (mk_gemm_ar): C_final = A @ B +
     sum of the world-1 staged peer partials [world-1, M, N], fp32 adds."""
     _bf16(A, "A"); _bf16(B, "B"); _bf16(C_final, "C_final")
@@ -118,9 +121,18 @@ def gemm_ar(A, B, C_final, peer_src, peer_recv, world: int, flags, stage_order, 
     N = B.shape[1]
     args = GemmArArgs(_ptr(A), _ptr(B), _ptr(C_final), _ptr(peer_src), _ptr(peer_recv), M, N, K, world, _ptr(flags),
                       _ptr(stage_order), epoch, int(gated), num_producers, num_cus, spin_limit, _ptr(error_word),
-                      _ptr(stage_counters), _ptr(done_flags), *_ws(split_ws, A.device))
+                      _ptr(stage_counters), _ptr(done_flags), *_ws(split_ws, A.device), _ptr(epoch_ptr))
     capi.call("mk_gemm_ar", args, _stream())
     return C_final
+
+
+def epoch_advance(epoch_word: torch.Tensor) -> torch.Tensor:
+    """*epoch_word += 1 on the current stream, skipping 0 (mk_epoch_advance);
+    epoch_word: a one-element int32/uint32 device tensor."""
+    if not epoch_word.is_cuda or epoch_word.numel() != 1 or epoch_word.element_size() != 4:
+        raise ValueError("epoch_word must be a one-element 32-bit device tensor")
+    capi.check("mk_epoch_advance", capi.lib().mk_epoch_advance(_ptr(epoch_word), C.c_void_p(_stream() or None)))
+    return epoch_word
 
 
 def moe_build_indices(topk_ids: np.ndarray, gates: np.ndarray, e0: int, n_local: int,

@@ -408,3 +408,98 @@ def test_gemm_split_tail_exchange_identity_exact(dev):
     I = torch.eye(n, dtype=torch.bfloat16, device=dev)
     X = wl.randn_bf16((n, 1536), 33).to(dev)
     assert torch.equal(ops.gemm(I, X, tile_m=256, num_cus=32).cpu(), X.cpu())
+
+
+@pytest.mark.parametrize("prod", [-1, 8])
+def test_ag_gemm_graph_replays_device_epoch(dev, prod):
+    """AllGather+GEMM recorded once in a HIP graph after mk_epoch_advance,
+    reading its epoch from that device word: each replay, with new shard
+    contents written between replays (and eager library work and
+    synchronizations in between), re-stages the shards under a new epoch and
+    gives the ungated GEMM's bits on them.  Waits are bounded."""
+    _say(f"ag_gemm graph replays, device epoch, producers={prod}")
+    cfg, A, B, order = _ag_case(dev)
+    Bd = B.to(dev)
+    shards = A.to(dev)
+    A_full = torch.zeros_like(shards)
+    C = torch.empty((cfg.M, cfg.N), dtype=torch.bfloat16, device=dev)
+    flags = torch.zeros(cfg.M // 128, dtype=torch.int32, device=dev)
+    counters = torch.zeros_like(flags)
+    err = torch.zeros(1, dtype=torch.int32, device=dev)
+    word = torch.zeros(1, dtype=torch.int32, device=dev)
+    od = order.to(dev)
+
+    def step():
+        ops.epoch_advance(word)
+        ops.ag_gemm(shards, A_full, Bd, C, flags, od, epoch=0, num_producers=prod, stage_counters=counters,
+                    spin_limit=4_000_000, error_word=err, epoch_ptr=word)
+
+    step()  # eager: epoch 1
+    torch.cuda.synchronize()
+    assert int(word.item()) == 1 and (flags.cpu() == 1).all()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        step()
+    gen = torch.Generator().manual_seed(11)
+    for rep in range(4):
+        new = (torch.randn(cfg.M, cfg.K, generator=gen) / cfg.K ** 0.5).to(torch.bfloat16)
+        shards.copy_(new.to(dev))
+        C.fill_(7.0)
+        g.replay()
+        torch.cuda.synchronize()
+        assert int(err.item()) == 0
+        epoch = 2 + rep  # the capture itself launched nothing
+        assert int(word.item()) == epoch
+        assert (flags.cpu() == epoch).all()
+        assert torch.equal(A_full.cpu(), new)
+        ref = torch.empty_like(C)
+        ops.ag_gemm(None, A_full, Bd, ref, None, None, epoch=1, gated=False, num_producers=0)
+        torch.cuda.synchronize()
+        assert torch.equal(C.cpu(), ref.cpu()), rep
+
+
+def test_gemm_rs_graph_replays_device_epoch(dev):
+    """GEMM+reduce-scatter with cooperative staging in a HIP graph, epoch
+    from a device word: every replay with new peer partials folds them (the
+    owned slice equals an eager run with a host epoch on the same data)."""
+    _say("gemm_rs graph replays, device epoch")
+    cfg = wl.RsCfg(world=8, rank=3, M=2048, K=256, N=512)
+    A, B, peers, order = wl.rs_inputs(cfg)
+    rows = cfg.M // cfg.world
+    Ad, Bd, pd = A.to(dev), B.to(dev), peers.to(dev)
+    nfl = (cfg.world - 1) * rows // 128
+    od = torch.from_numpy(order).to(dev)
+    work = torch.zeros((cfg.M, cfg.N), dtype=torch.bfloat16, device=dev)
+    out = torch.zeros((rows, cfg.N), dtype=torch.bfloat16, device=dev)
+    recv = torch.zeros_like(pd)
+    flags = torch.zeros(nfl, dtype=torch.int32, device=dev)
+    counters = torch.zeros_like(flags)
+    err = torch.zeros(1, dtype=torch.int32, device=dev)
+    word = torch.zeros(1, dtype=torch.int32, device=dev)
+
+    def step():
+        ops.epoch_advance(word)
+        ops.gemm_rs(Ad, Bd, work, out, pd, recv, cfg.world, cfg.rank, flags, od, epoch=0, num_producers=-1,
+                    stage_counters=counters, spin_limit=4_000_000, error_word=err, epoch_ptr=word)
+
+    step()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        step()
+    gen = torch.Generator().manual_seed(12)
+    e_flags = torch.zeros_like(flags)
+    e_counters = torch.zeros_like(flags)
+    for rep in range(3):
+        new = (torch.randn(peers.shape, generator=gen) * 0.5).to(torch.bfloat16)
+        pd.copy_(new.to(dev))
+        out.fill_(5.0)
+        g.replay()
+        torch.cuda.synchronize()
+        assert int(err.item()) == 0 and (flags.cpu() == 2 + rep).all()
+        assert torch.equal(recv.cpu(), new)
+        ref = torch.zeros_like(out)
+        ops.gemm_rs(Ad, Bd, torch.zeros_like(work), ref, pd, torch.zeros_like(recv), cfg.world, cfg.rank, e_flags, od,
+                    epoch=1 + rep, num_producers=-1, stage_counters=e_counters)
+        torch.cuda.synchronize()
+        assert torch.equal(out.cpu(), ref.cpu()), rep
