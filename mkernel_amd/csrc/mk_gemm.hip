@@ -244,7 +244,8 @@ __device__ __forceinline__ void store_rows(uint16_t* base, int64_t ldc, f32x16 (
 // fp32, pitch padded by 16 bytes) and comes back 8 columns per lane with
 // consecutive lanes along a row; the lane then loads the same 8 columns of
 // every peer's bf16 partial (16 bytes per peer: whole row segments per
-// instruction, 4 peers' loads in flight), adds them in rank order in fp32
+// instruction, 4 peers' loads in flight, the remainder as one more group),
+// adds them in rank order in fp32
 // (deterministic, one rounding) and stores 16 bytes of the owned output.
 // In the accumulator layout every load and store instruction would touch
 // 32 rows with 8 bytes each.
@@ -294,12 +295,21 @@ __device__ __forceinline__ void reduce_rows(const GemmKParams& p, f32x16 (&acc)[
           x[6] += bf16_lo(v[u].w); x[7] += bf16_hi(v[u].w);
         }
       }
-      for (; q < np; ++q) {
-        const uint4 v = *reinterpret_cast<const uint4*>(src + q * peer_stride);
-        x[0] += bf16_lo(v.x); x[1] += bf16_hi(v.x);
-        x[2] += bf16_lo(v.y); x[3] += bf16_hi(v.y);
-        x[4] += bf16_lo(v.z); x[5] += bf16_hi(v.z);
-        x[6] += bf16_lo(v.w); x[7] += bf16_hi(v.w);
+      if (q < np) {
+        // the last np - q peers as one more group in flight (indices
+        // clamped to the last peer, so no branch splits the loads)
+        uint4 v[kPeers];
+#pragma unroll
+        for (int u = 0; u < kPeers; ++u)
+          v[u] = *reinterpret_cast<const uint4*>(src + (int64_t)min(q + u, np - 1) * peer_stride);
+#pragma unroll
+        for (int u = 0; u < kPeers; ++u)
+          if (q + u < np) {
+            x[0] += bf16_lo(v[u].x); x[1] += bf16_hi(v[u].x);
+            x[2] += bf16_lo(v[u].y); x[3] += bf16_hi(v[u].y);
+            x[4] += bf16_lo(v[u].z); x[5] += bf16_hi(v[u].z);
+            x[6] += bf16_lo(v[u].w); x[7] += bf16_hi(v[u].w);
+          }
       }
       uint4 o;
       o.x = pack_bf16x2(x[0], x[1]); o.y = pack_bf16x2(x[2], x[3]);
