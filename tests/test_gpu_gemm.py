@@ -503,3 +503,53 @@ def test_gemm_rs_graph_replays_device_epoch(dev):
                     epoch=1 + rep, num_producers=-1, stage_counters=e_counters)
         torch.cuda.synchronize()
         assert torch.equal(out.cpu(), ref.cpu()), rep
+
+
+def test_gemm_ar_graph_replays_device_epoch(dev):
+    """GEMM + all-reduce in a HIP graph after mk_epoch_advance: each replay
+    with new peer partials stages them under a new epoch, publishes every
+    tile's done flag with it, and gives the bits of an eager launch with a
+    host epoch on the same data."""
+    _say("gemm_ar graph replays, device epoch")
+    world, M, N, K = 8, 512, 512, 256
+    A = wl.randn_bf16((M, K), 40, K ** -0.5).to(dev)
+    B = wl.randn_bf16((K, N), 41, K ** -0.5).to(dev)
+    peers = wl.randn_bf16((world - 1, M, N), 42, 0.5).to(dev)
+    nflags = (world - 1) * M // 128
+    ntiles = (M // 256) * (N // 256)
+    order = torch.from_numpy(wl.stage_order(nflags, 3)).to(dev)
+    recv = torch.zeros_like(peers)
+    flags = torch.zeros(nflags, dtype=torch.int32, device=dev)
+    counters = torch.zeros_like(flags)
+    done = torch.zeros(ntiles, dtype=torch.int32, device=dev)
+    err = torch.zeros(1, dtype=torch.int32, device=dev)
+    word = torch.zeros(1, dtype=torch.int32, device=dev)
+    C = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+
+    def step():
+        ops.epoch_advance(word)
+        ops.gemm_ar(A, B, C, peers, recv, world, flags, order, epoch=0, num_producers=-1, stage_counters=counters,
+                    done_flags=done, spin_limit=4_000_000, error_word=err, epoch_ptr=word)
+
+    step()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        step()
+    gen = torch.Generator().manual_seed(13)
+    e_flags, e_counters, e_done = torch.zeros_like(flags), torch.zeros_like(flags), torch.zeros_like(done)
+    for rep in range(3):
+        new = (torch.randn(peers.shape, generator=gen) * 0.5).to(torch.bfloat16)
+        peers.copy_(new.to(dev))
+        C.fill_(3.0)
+        g.replay()
+        torch.cuda.synchronize()
+        epoch = 2 + rep
+        assert int(err.item()) == 0
+        assert (flags.cpu() == epoch).all() and (done.cpu() == epoch).all()
+        assert torch.equal(recv.cpu(), new)
+        ref = torch.empty_like(C)
+        ops.gemm_ar(A, B, ref, peers, torch.zeros_like(recv), world, e_flags, order, epoch=1 + rep,
+                    num_producers=-1, stage_counters=e_counters, done_flags=e_done)
+        torch.cuda.synchronize()
+        assert torch.equal(C.cpu(), ref.cpu()), rep
