@@ -45,7 +45,7 @@ typedef struct mk_gemm_args {
   void* C;        /* bf16 [M, ldc] */
   int64_t M, N, K;
   int64_t lda, ldb, ldc;
-  int32_t num_cus; /* persistent grid size; 0 = every CU of the device */
+  int32_t num_cus; /* persistent grid size; 0 = every CU of the device; at most the CU count */
   int32_t tile_m;  /* 0 = auto, else 128 or 256 */
   int32_t waves;   /* waves per workgroup: 0 = auto, 4 (one per SIMD) or 8 (two per SIMD) */
   void* split_ws;          /* optional K-split workspace (see mk_query_workspace_bytes);
@@ -92,7 +92,8 @@ typedef struct mk_ag_gemm_args {
   uint32_t epoch;               /* value a ready flag must hold (never 0) */
   int32_t gated;
   int32_t num_producers;
-  int32_t num_cus;              /* total workgroups (producers + compute); 0 = all CUs */
+  int32_t num_cus;              /* total workgroups (producers + compute); 0 = all CUs; never more
+                                   than the device's CUs (every workgroup must be resident) */
   uint32_t spin_limit;          /* polls before a wait gives up; 0 = unbounded */
   uint32_t* error_word;         /* optional device word, bit0 set on timeout */
   uint32_t* stage_counters;     /* [M/128] piece counters for producers == -1; zero once, never reset */
@@ -105,6 +106,13 @@ typedef struct mk_ag_gemm_args {
    * mk_epoch_advance and this launch gates every replay on a new epoch with
    * no host work.  NULL = use `epoch`. */
   const uint32_t* epoch_ptr;
+  /* Number of leading stage_order positions whose 128-row blocks are
+   * already in A_full (this rank's own shard, written there by the caller
+   * as the reference bench does, bench/ag_gemm_bench.py:364-372): the
+   * staging publishes their flags without copying them, and A_shards is
+   * not read for them.  0 = every block is copied.  Needs stage_order when
+   * non-zero. */
+  int32_t n_present;
 } mk_ag_gemm_args;
 int mk_ag_gemm(const mk_ag_gemm_args* args, void* stream);
 
@@ -334,11 +342,16 @@ typedef struct mk_moe_combine_args {
 } mk_moe_combine_args;
 int mk_moe_combine(const mk_moe_combine_args* args, void* stream);
 
-/* slot_to_row[row_to_slot[r]] = r for every row with row_to_owner[r] >= 0:
- * turns the reference's producer-side table (row_to_slot) into the gather
- * table the combine reads. */
-int mk_moe_invert_slots(const int32_t* row_to_slot, const int32_t* row_to_owner, int64_t R_pad,
-                        int32_t* slot_to_row, void* stream);
+/* Turns the reference's producer-side tables (row_to_slot, row_to_owner;
+ * bench/dispatch_gemm_glu_combine_bench.py:264-279) into the gather table
+ * the combine reads: slot_to_row[0 .. slot_capacity) is first set to -1,
+ * then slot_to_row[row_to_slot[r]] = r for every row r with
+ * row_to_owner[r] == owner.  Rows of other owners (another GPU combines
+ * them) are left out, and the combine skips slots that stay -1.  A slot
+ * outside [0, slot_capacity) is not written; it sets bit 1 of *error_word
+ * when error_word is non-NULL. */
+int mk_moe_invert_slots(const int32_t* row_to_slot, const int32_t* row_to_owner, int64_t R_pad, int32_t owner,
+                        int64_t slot_capacity, int32_t* slot_to_row, uint32_t* error_word, void* stream);
 
 /* rb_rows[b] = number of rows r in [128b, 128b+128) with pull_indices[r][0] >= 0
  * (device, from the reference's pull table). */
@@ -418,7 +431,8 @@ const char* mk_last_error_string(void);
 int mk_epoch_advance(uint32_t* epoch_ptr, void* stream);
 
 /* ABI version, bumped on any signature change (2: split_ws fields; 4: MoE
- * `sizes`; 5: epoch_ptr). */
+ * `sizes`; 5: epoch_ptr; 6: mk_ag_gemm n_present, mk_moe_invert_slots owner
+ * and slot capacity). */
 int32_t mk_abi_version(void);
 
 #ifdef __cplusplus

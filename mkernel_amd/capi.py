@@ -13,6 +13,7 @@ from pathlib import Path
 LIB_PATH = Path(__file__).resolve().parent / "libmk.so"
 
 ROW_BLOCK = 128
+ABI_VERSION = 6  # include/mk.h mk_abi_version(): the structures below match this layout
 
 EXPORTS = (
     "mk_gemm",
@@ -63,7 +64,8 @@ class AgGemmArgs(C.Structure):
                 ("M", i64), ("N", i64), ("K", i64),
                 ("flags", vp), ("stage_order", vp), ("epoch", u32), ("gated", i32),
                 ("num_producers", i32), ("num_cus", i32), ("spin_limit", u32), ("error_word", vp),
-                ("stage_counters", vp), ("split_ws", vp), ("split_ws_bytes", i64), ("epoch_ptr", vp)]
+                ("stage_counters", vp), ("split_ws", vp), ("split_ws_bytes", i64), ("epoch_ptr", vp),
+                ("n_present", i32)]
 
 
 class GemmRsArgs(C.Structure):
@@ -146,7 +148,7 @@ def lib() -> C.CDLL:
         L.mk_moe_index_workspace_bytes.restype = i64
         L.mk_moe_build_indices_dev.argtypes = [vp, vp]
         L.mk_moe_build_indices_dev.restype = C.c_int
-        L.mk_moe_invert_slots.argtypes = [vp, vp, i64, vp, vp]
+        L.mk_moe_invert_slots.argtypes = [vp, vp, i64, i32, i64, vp, vp, vp]
         L.mk_moe_invert_slots.restype = C.c_int
         L.mk_moe_tile_rows.argtypes = [vp, i64, vp, vp]
         L.mk_moe_tile_rows.restype = C.c_int
@@ -164,6 +166,9 @@ def lib() -> C.CDLL:
         L.mk_epoch_advance.restype = i32
         L.mk_abi_version.argtypes = []
         L.mk_abi_version.restype = i32
+        if L.mk_abi_version() != ABI_VERSION:
+            raise RuntimeError(f"{LIB_PATH} has ABI {L.mk_abi_version()}, this binding needs {ABI_VERSION}: "
+                               "rebuild with __graft_entry__.build()")
         _lib = L
     return _lib
 

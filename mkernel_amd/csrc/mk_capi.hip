@@ -60,6 +60,16 @@ int device_info(DevInfo* out) {
   return MK_OK;
 }
 
+// Persistent grid size: 0 = every CU.  More workgroups than CUs is refused:
+// the flag waits, cooperative staging and the K-split exchange all assume
+// that every workgroup of the launch is resident at once (one per CU).
+int grid_total(int num_cus, const DevInfo& d, const char* fn, int* total) {
+  if (num_cus < 0 || num_cus > d.cus)
+    return fail(MK_EINVAL, "%s: num_cus=%d must be 0 (every CU) or at most the device's %d CUs", fn, num_cus, d.cus);
+  *total = num_cus > 0 ? num_cus : d.cus;
+  return MK_OK;
+}
+
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 void fill_common(mk::GemmKParams& p) {
@@ -139,7 +149,7 @@ extern "C" {
 
 const char* mk_last_error_string(void) { return g_err.c_str(); }
 
-int32_t mk_abi_version(void) { return 5; }
+int32_t mk_abi_version(void) { return 6; }
 
 int mk_epoch_advance(uint32_t* epoch_ptr, void* stream) {
   if (!epoch_ptr) return fail(MK_EINVAL, "mk_epoch_advance: null argument");
@@ -198,7 +208,8 @@ int mk_gemm(const mk_gemm_args* a, void* stream) {
   p.M = (int)a->M; p.N = (int)a->N; p.K = (int)a->K;
   p.tiles_m = (int)(a->M / bm);
   p.tiles_n = (int)(a->N / 256);
-  const int total = a->num_cus > 0 ? a->num_cus : d.cus;
+  int total;
+  if (int rc = grid_total(a->num_cus, d, "mk_gemm", &total)) return rc;
   set_grid(p, total, 0, p.tiles_m * p.tiles_n);
   if (a->waves) p.waves = a->waves;
   if (int rc = check_ws(a->split_ws, a->split_ws_bytes, "mk_gemm")) return rc;
@@ -227,9 +238,14 @@ int mk_ag_gemm(const mk_ag_gemm_args* a, void* stream) {
     return fail(MK_EINVAL, "mk_ag_gemm: staging needs A_shards");
   const bool coop = a->gated && a->num_producers < 0;
   if (coop && !a->stage_counters) return fail(MK_EINVAL, "mk_ag_gemm: cooperative staging needs stage_counters");
-  const int total = a->num_cus > 0 ? a->num_cus : d.cus;
+  int total;
+  if (int rc = grid_total(a->num_cus, d, "mk_ag_gemm", &total)) return rc;
   const int n_prod = (a->gated && a->num_producers > 0) ? a->num_producers : 0;
   if (n_prod >= total) return fail(MK_EINVAL, "mk_ag_gemm: num_producers (%d) leaves no compute workgroups", n_prod);
+  if (a->n_present < 0 || a->n_present > nflags)
+    return fail(MK_EINVAL, "mk_ag_gemm: n_present=%d must be in [0, M/128]", a->n_present);
+  if (a->n_present > 0 && !a->stage_order)
+    return fail(MK_EINVAL, "mk_ag_gemm: n_present needs stage_order (the present blocks are its first entries)");
   mk::GemmKParams p;
   fill_common(p);
   p.A = static_cast<const uint16_t*>(a->A_full);
@@ -254,6 +270,7 @@ int mk_ag_gemm(const mk_ag_gemm_args* a, void* stream) {
       p.st_cols = (int)a->K;
       p.st_nblocks = (int)nflags;
       p.st_order = a->stage_order;
+      p.st_present = a->n_present;
       p.st_flags = a->flags;
       p.st_counters = a->stage_counters;
       p.st_coop = coop ? (a->num_producers == -1 ? 2 : 1) : 0;  // -1: halves alternate windows
@@ -279,7 +296,8 @@ int mk_gemm_rs(const mk_gemm_rs_args* a, void* stream) {
   const int npeers = a->world - 1;
   if (npeers > 0 && !a->peer_recv) return fail(MK_EINVAL, "mk_gemm_rs: peer_recv is null");
   const int own_rows = (int)(a->M / a->world);
-  const int total = a->num_cus > 0 ? a->num_cus : d.cus;
+  int total;
+  if (int rc = grid_total(a->num_cus, d, "mk_gemm_rs", &total)) return rc;
   if (a->num_producers < -2) return fail(MK_EINVAL, "mk_gemm_rs: num_producers must be >= -2");
   const bool coop = a->gated && npeers > 0 && a->num_producers < 0;
   const int n_prod = (a->gated && npeers > 0 && a->num_producers > 0) ? a->num_producers : 0;
@@ -343,7 +361,8 @@ int mk_gemm_ar(const mk_gemm_ar_args* a, void* stream) {
   const int64_t nflags = (int64_t)npeers * (a->M / 128);
   if (a->stage_order && nflags + a->M / bm > 8192)
     return fail(MK_ESHAPE, "mk_gemm_ar: too many flags for the arrival-order schedule");
-  const int total = a->num_cus > 0 ? a->num_cus : d.cus;
+  int total;
+  if (int rc = grid_total(a->num_cus, d, "mk_gemm_ar", &total)) return rc;
   if (a->num_producers < -2) return fail(MK_EINVAL, "mk_gemm_ar: num_producers must be >= -2");
   const bool gated = a->gated && npeers > 0;
   const bool coop = gated && a->num_producers < 0;
@@ -547,7 +566,8 @@ static int grouped_gemm_impl(const void* A, const void* W, void* out, const int3
   p.gather_rows = n_src_rows;
   p.gather_tps = tokens_per_src;
   p.gather_devs = devs_per_node;
-  const int total = num_cus > 0 ? num_cus : d.cus;
+  int total;
+  if (int rc = grid_total(num_cus, d, "mk_moe_grouped_gemm", &total)) return rc;
   set_grid(p, total, 0, p.tiles_m * p.tiles_n);
   // Few column tiles (GEMM1: 2I / 512 = 8): walk all row blocks of one
   // weight column slice together, so an expert's row blocks share its weight
@@ -611,14 +631,18 @@ int mk_moe_combine(const mk_moe_combine_args* a, void* stream) {
   return e == hipSuccess ? MK_OK : hip_fail(e, "mk_moe_combine launch");
 }
 
-int mk_moe_invert_slots(const int32_t* row_to_slot, const int32_t* row_to_owner, int64_t R_pad,
-                        int32_t* slot_to_row, void* stream) {
-  if (R_pad < 0) return fail(MK_EINVAL, "mk_moe_invert_slots: R_pad < 0");
-  if (R_pad == 0) return MK_OK;
-  if (!row_to_slot || !row_to_owner || !slot_to_row) return fail(MK_EINVAL, "mk_moe_invert_slots: null argument");
+int mk_moe_invert_slots(const int32_t* row_to_slot, const int32_t* row_to_owner, int64_t R_pad, int32_t owner,
+                        int64_t slot_capacity, int32_t* slot_to_row, uint32_t* error_word, void* stream) {
+  if (R_pad < 0 || slot_capacity < 0) return fail(MK_EINVAL, "mk_moe_invert_slots: R_pad and slot_capacity must be >= 0");
+  if (slot_capacity > (1LL << 31)) return fail(MK_ESHAPE, "mk_moe_invert_slots: slot_capacity above 2^31");
+  if (owner < 0) return fail(MK_EINVAL, "mk_moe_invert_slots: owner must be >= 0");
+  if (R_pad == 0 && slot_capacity == 0) return MK_OK;
+  if ((R_pad > 0 && (!row_to_slot || !row_to_owner)) || (slot_capacity > 0 && !slot_to_row))
+    return fail(MK_EINVAL, "mk_moe_invert_slots: null argument");
   DevInfo d;
   if (int rc = device_info(&d)) return rc;
-  hipError_t e = mk::launch_invert_slots(row_to_slot, row_to_owner, R_pad, slot_to_row, static_cast<hipStream_t>(stream));
+  hipError_t e = mk::launch_invert_slots(row_to_slot, row_to_owner, R_pad, owner, slot_capacity, slot_to_row,
+                                         error_word, static_cast<hipStream_t>(stream));
   return e == hipSuccess ? MK_OK : hip_fail(e, "mk_moe_invert_slots launch");
 }
 

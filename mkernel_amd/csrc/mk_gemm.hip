@@ -31,6 +31,7 @@
 // the other's MFMAs).
 #include "mk_device.h"
 #include "mk_internal.h"
+#include "mk_once.h"
 
 namespace mk {
 
@@ -129,7 +130,8 @@ __device__ void producer_role(const GemmKParams& p, int pid) {
   const int64_t block_elems = (int64_t)kFlagRows * p.st_cols;
   for (int i = pid; i < p.st_nblocks; i += p.n_prod) {
     const int b = p.st_order ? p.st_order[i] : i;
-    copy_wt<NT, 16>(p.st_src + (int64_t)b * block_elems, p.st_dst + (int64_t)b * block_elems, block_elems / 8);
+    if (i >= p.st_present)
+      copy_wt<NT, 16>(p.st_src + (int64_t)b * block_elems, p.st_dst + (int64_t)b * block_elems, block_elems / 8);
     // every wave's write-through stores performed, then one publication
     wait_vmem_all();
     __syncthreads();
@@ -156,7 +158,9 @@ __device__ void coop_stage(const GemmKParams& p, int stride, int& q, int& batch,
     const int pos = qq / kPieces, piece = qq % kPieces;
     const int b = p.st_order ? p.st_order[pos] : pos;
     const int64_t off = (int64_t)b * block_elems + (int64_t)piece * piece_vec * 8;
-    copy_wt<NT, 16>(p.st_src + off, p.st_dst + off, piece_vec);
+    // blocks at the first st_present positions are already in place (this
+    // rank's own shard): counted and published, not copied
+    if (pos >= p.st_present) copy_wt<NT, 16>(p.st_src + off, p.st_dst + off, piece_vec);
     return b;
   };
   // The counter increments form one chain per block; each is made after
@@ -692,7 +696,9 @@ __device__ __forceinline__ void compute_role(const GemmKParams& p, int cons_id, 
 
     const uint16_t* Bp = p.B;
     if (p.rb_expert) {
-      const int e = __builtin_amdgcn_readfirstlane(p.rb_expert[tm]);
+      // clamped like the expert_rows walk: a stale table entry must not
+      // form a B base outside the weight tensor
+      const int e = __builtin_amdgcn_readfirstlane(min(max(p.rb_expert[tm], 0), p.n_experts - 1));
       Bp += (int64_t)e * p.b_expert_stride;
     } else if (p.expert_rows) {
       // Expert whose padded row range holds row m0 (prefix walk over the
@@ -1258,12 +1264,18 @@ hipError_t launch_epoch_advance(uint32_t* epoch_ptr, hipStream_t stream) {
 template <int BM, int WAVES, int EPI, int BN>
 static hipError_t launch_t(const GemmKParams& p, hipStream_t stream) {
   using C = Cfg<BM, WAVES, BN>;
-  static bool attr_set = false;  // once per process (one attribute per kernel)
-  if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_kernel<BM, WAVES, EPI, BN>),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, C::LDS_BYTES);
+  // The dynamic-LDS limit is raised once per device and kernel.  Two
+  // threads that both find the flag clear both set the attribute, which is
+  // harmless; a launch never runs before its device's attribute is set.
+  static PerDeviceFlag attr_set;
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (!attr_set.is_set(dev)) {
+    e = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_kernel<BM, WAVES, EPI, BN>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, C::LDS_BYTES);
     if (e != hipSuccess) return e;
-    attr_set = true;
+    attr_set.set(dev);
   }
   hipLaunchKernelGGL((gemm_kernel<BM, WAVES, EPI, BN>), dim3(p.n_prod + p.n_cons), dim3(C::NT), C::LDS_BYTES,
                      stream, p);

@@ -53,6 +53,7 @@ struct GemmKParams {
   const uint16_t* st_src;
   uint16_t* st_dst;
   int st_cols, st_nblocks;
+  int st_present;           // stage positions < st_present hold blocks already in st_dst: published, not copied
   const int* st_order;
   uint32_t* st_flags;
   uint32_t* st_counters;    // cooperative staging: pieces completed per block (mod kPieces)
@@ -106,7 +107,7 @@ int64_t index_workspace_bytes(int T, int topk, int n_local);
 hipError_t launch_mfma_ceiling(int64_t iters, int n_wg, uint32_t seed, float* sink, uint64_t* clocks,
                                hipStream_t stream);
 int probe_threads();
-hipError_t launch_invert_slots(const int* row_to_slot, const int* row_to_owner, int64_t R_pad, int* slot_to_row,
-                               hipStream_t stream);
+hipError_t launch_invert_slots(const int* row_to_slot, const int* row_to_owner, int64_t R_pad, int owner,
+                               int64_t slot_capacity, int* slot_to_row, uint32_t* err, hipStream_t stream);
 
 }  // namespace mk

@@ -55,9 +55,11 @@ __global__ __launch_bounds__(kThreads) void combine_kernel(CombineKParams p) {
 #pragma unroll
   for (int k = 0; k < kMaxSlots; ++k)
     if (few && k < n) rows[k] = p.slot_to_row[s0 + k];
+  // a slot whose row is -1 was not produced on this GPU (another owner's
+  // combine covers it): it contributes nothing
 #pragma unroll
   for (int k = 0; k < kMaxSlots; ++k)
-    if (few && k < n) wts[k] = p.row_weight[rows[k]];
+    if (few && k < n) wts[k] = rows[k] >= 0 ? p.row_weight[rows[k]] : 0.f;
   for (int64_t c = threadIdx.x; c < vec; c += kThreads) {
     float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
     auto add = [&](float w, const uint4& v) {
@@ -74,13 +76,14 @@ __global__ __launch_bounds__(kThreads) void combine_kernel(CombineKParams p) {
       uint4 v[kMaxSlots];
 #pragma unroll
       for (int k = 0; k < kMaxSlots; ++k)
-        if (k < n) v[k] = *reinterpret_cast<const uint4*>(p.y_expert + (int64_t)rows[k] * p.H + c * 8);
+        if (k < n && rows[k] >= 0) v[k] = *reinterpret_cast<const uint4*>(p.y_expert + (int64_t)rows[k] * p.H + c * 8);
 #pragma unroll
       for (int k = 0; k < kMaxSlots; ++k)
-        if (k < n) add(wts[k], v[k]);
+        if (k < n && rows[k] >= 0) add(wts[k], v[k]);
     } else {
       for (int s = s0; s < s1; ++s) {
         const int row = p.slot_to_row[s];
+        if (row < 0) continue;
         add(p.row_weight[row], *reinterpret_cast<const uint4*>(p.y_expert + (int64_t)row * p.H + c * 8));
       }
     }
@@ -119,17 +122,29 @@ hipError_t launch_tile_rows(const int* pull, int64_t R_pad, int* rb_rows, hipStr
   return hipGetLastError();
 }
 
-__global__ void invert_slots_kernel(const int* row_to_slot, const int* row_to_owner, int64_t R_pad,
-                                    int* slot_to_row) {
-  const int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (r < R_pad && row_to_owner[r] >= 0) slot_to_row[row_to_slot[r]] = (int)r;
+__global__ void fill_i32_kernel(int* dst, int64_t n, int value) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) dst[i] = value;
 }
 
-hipError_t launch_invert_slots(const int* row_to_slot, const int* row_to_owner, int64_t R_pad, int* slot_to_row,
-                               hipStream_t stream) {
-  if (R_pad == 0) return hipSuccess;
-  hipLaunchKernelGGL(invert_slots_kernel, dim3((unsigned)((R_pad + 255) / 256)), dim3(256), 0, stream, row_to_slot,
-                     row_to_owner, R_pad, slot_to_row);
+// Rows of `owner` only; a slot outside [0, cap) is skipped and reported.
+__global__ void invert_slots_kernel(const int* row_to_slot, const int* row_to_owner, int64_t R_pad, int owner,
+                                    int64_t cap, int* slot_to_row, uint32_t* err) {
+  const int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (r >= R_pad || row_to_owner[r] != owner) return;
+  const int s = row_to_slot[r];
+  if (s >= 0 && s < cap) slot_to_row[s] = (int)r;
+  else if (err) __hip_atomic_fetch_or(err, 2u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+hipError_t launch_invert_slots(const int* row_to_slot, const int* row_to_owner, int64_t R_pad, int owner,
+                               int64_t cap, int* slot_to_row, uint32_t* err, hipStream_t stream) {
+  // a fill kernel, not hipMemsetAsync, so the pair can be recorded in a graph
+  if (cap > 0)
+    hipLaunchKernelGGL(fill_i32_kernel, dim3((unsigned)((cap + 255) / 256)), dim3(256), 0, stream, slot_to_row, cap, -1);
+  if (R_pad > 0)
+    hipLaunchKernelGGL(invert_slots_kernel, dim3((unsigned)((R_pad + 255) / 256)), dim3(256), 0, stream, row_to_slot,
+                       row_to_owner, R_pad, owner, cap, slot_to_row, err);
   return hipGetLastError();
 }
 

@@ -36,25 +36,30 @@ def cu_count() -> int:
 _split_ws: dict = {}
 
 
-def split_workspace(device=None) -> torch.Tensor:
-    """The per-device K-split workspace the GEMM entry points use by default:
-    mk_query_workspace_bytes() bytes, zero-filled once (every launch leaves
-    it zeroed).  Launches sharing it must be stream-ordered; pass an explicit
-    ``split_ws`` to run GEMMs concurrently on several streams."""
+def split_workspace(device=None, stream=None) -> torch.Tensor:
+    """The K-split workspace the GEMM entry points use by default: one per
+    (device, stream), mk_query_workspace_bytes() bytes, zero-filled once
+    (every launch leaves it zeroed).  Launches on one stream are ordered, so
+    they can share it; launches on different streams get different ones.
+    ``stream``: a torch stream, default the current stream of the device."""
     dev = torch.device("cuda", torch.cuda.current_device() if device is None else torch.device(device).index or 0)
-    ws = _split_ws.get(dev)
+    if stream is None:
+        stream = torch.cuda.current_stream(dev)
+    key = (dev, stream.cuda_stream)
+    ws = _split_ws.get(key)
     if ws is None:
         n = int(capi.lib().mk_query_workspace_bytes(0, 0, 0, 0))
         if n < 0:
             raise capi.MkError("mk_query_workspace_bytes", n, capi.lib().mk_last_error_string().decode())
         ws = torch.zeros(n, dtype=torch.uint8, device=dev)
-        _split_ws[dev] = ws
+        _split_ws[key] = ws
     return ws
 
 
 def _ws(split_ws, device) -> tuple:
-    """(pointer, bytes) of the K-split workspace: the default one, an explicit
-    tensor, or none at all when split_ws is False."""
+    """(pointer, bytes) of the K-split workspace: the default one of the
+    device's current stream, an explicit tensor, or none at all when
+    split_ws is False."""
     if split_ws is False:
         return None, 0
     ws = split_workspace(device) if split_ws is None or split_ws is True else split_ws
@@ -78,20 +83,21 @@ def gemm(A: torch.Tensor, B: torch.Tensor, out: torch.Tensor | None = None, num_
 
 def ag_gemm(A_shards, A_full, B, C_out, flags, stage_order, epoch: int, gated: bool = True,
             num_producers: int = -1, num_cus: int = 0, spin_limit: int = 0, error_word=None,
-            stage_counters=None, split_ws=None, epoch_ptr=None) -> torch.Tensor:
+            stage_counters=None, split_ws=None, epoch_ptr=None, n_present: int = 0) -> torch.Tensor:
     """Flag-gated AllGather+GEMM; see include/mk.h mk_ag_gemm.  epoch_ptr: an
     optional uint32 device word read for the epoch instead of `epoch`
     (advanced by epoch_advance, e.g. inside a recorded graph).  num_producers
     -1 (default) stages cooperatively, the two halves of the grid taking
     turns to copy ahead; -2 stages cooperatively with every workgroup copying
     an even share before every round.  Both need stage_counters (int32
-    [M/128], zeroed once)."""
+    [M/128], zeroed once).  n_present: the first n_present blocks of
+    stage_order are already in A_full (published, not copied)."""
     _bf16(A_full, "A_full"); _bf16(B, "B"); _bf16(C_out, "C")
     M, K = A_full.shape
     N = B.shape[1]
     args = AgGemmArgs(_ptr(A_shards), _ptr(A_full), _ptr(B), _ptr(C_out), M, N, K, _ptr(flags), _ptr(stage_order),
                       epoch, int(gated), num_producers, num_cus, spin_limit, _ptr(error_word), _ptr(stage_counters),
-                      *_ws(split_ws, A_full.device), _ptr(epoch_ptr))
+                      *_ws(split_ws, A_full.device), _ptr(epoch_ptr), n_present)
     capi.call("mk_ag_gemm", args, _stream())
     return C_out
 
@@ -260,9 +266,13 @@ def moe_tile_rows(pull, rb_rows):
     return rb_rows
 
 
-def moe_invert_slots(row_to_slot, row_to_owner, slot_to_row):
+def moe_invert_slots(row_to_slot, row_to_owner, slot_to_row, owner: int = 0, error_word=None):
+    """slot_to_row[:] = -1, then slot_to_row[row_to_slot[r]] = r for the rows
+    of `owner` (mk_moe_invert_slots); slots past slot_to_row's length set
+    bit 1 of error_word."""
     capi.check("mk_moe_invert_slots", capi.lib().mk_moe_invert_slots(
-        _ptr(row_to_slot), _ptr(row_to_owner), row_to_slot.numel(), _ptr(slot_to_row), C.c_void_p(_stream() or None)))
+        _ptr(row_to_slot), _ptr(row_to_owner), row_to_slot.numel(), owner, slot_to_row.numel(), _ptr(slot_to_row),
+        _ptr(error_word), C.c_void_p(_stream() or None)))
     return slot_to_row
 
 

@@ -85,6 +85,54 @@ def test_config3_gemm_rs_full(dev):
     assert (work.cpu()[own0:own0 + rows] == 0).all()
 
 
+def test_config4_grouped_gemm1_full(dev):
+    """Config 4: dispatch + grouped GEMM1 (gate|up, no SwiGLU) at full size —
+    4096 tokens x 7168, W1 [32, 7168, 4096], R_pad rows.  The fused-gather
+    launch (rows read through the pull table) must equal permute + GEMM bit
+    for bit over every row, with the expert taken from either table; sampled
+    128-row blocks are checked against the oracle with the block's expert
+    from the pull table, and padding rows come out zero (reference
+    src/dispatch_gemm.cu:207-408, check bench/dispatch_gemm_bench.py:463-487)."""
+    _say("full config 4 dispatch + grouped gemm1")
+    cfg = wl.MoeCfg()
+    tokens, ids, gates, w1, _ = wl.moe_inputs(cfg, device=dev, with_w2=False)
+    idx = ops.moe_build_indices(ids, gates, cfg.e0, cfg.n_local)
+    d = {k: torch.from_numpy(np.ascontiguousarray(v)).to(dev) for k, v in idx.items() if isinstance(v, np.ndarray)}
+    R_pad, N = idx["R_pad"], 2 * cfg.I
+    fused = torch.full((R_pad, N), 7.0, dtype=torch.bfloat16, device=dev)
+    ops.moe_grouped_gemm(tokens, w1, fused, rb_expert=d["rb_expert"], rb_rows=d["rb_rows"], mode=0,
+                         gather_pull=d["pull_indices"])
+    fused_ppe = torch.full_like(fused, 7.0)
+    ops.moe_grouped_gemm(tokens, w1, fused_ppe, padded_tokens_per_expert=d["padded_tokens_per_expert"], mode=0,
+                         gather_pull=d["pull_indices"])
+    post = torch.empty((R_pad, cfg.H), dtype=torch.bfloat16, device=dev)
+    ops.moe_permute(tokens, d["pull_indices"], post)
+    unfused = torch.full_like(fused, 7.0)
+    ops.moe_grouped_gemm(post, w1, unfused, rb_expert=d["rb_expert"], rb_rows=d["rb_rows"], mode=0)
+    torch.cuda.synchronize()
+    assert torch.equal(fused, unfused), "fused gather differs from permute + GEMM"
+    assert torch.equal(fused, fused_ppe), "expert from padded counts differs from rb_expert"
+    assert torch.isfinite(fused.float()).all()
+    pull = idx["pull_indices"]
+    pad = torch.from_numpy(pull[:, 0] < 0)
+    assert (fused.cpu()[pad] == 0).all(), "padding rows must come out zero"
+    # sampled blocks vs the oracle, expert from the pull table's expert ranges
+    tok_cpu = tokens.cpu()
+    post_ref = om.permute_ref(tok_cpu, pull)
+    assert torch.equal(post.cpu(), post_ref)
+    bounds = np.cumsum(idx["padded_tokens_per_expert"])
+    rng = np.random.default_rng(15)
+    blocks = np.sort(rng.choice(R_pad // 128, size=8, replace=False))
+    out_cpu = fused.cpu()
+    for b in blocks:
+        e = int(np.searchsorted(bounds, b * 128, side="right"))
+        assert e == int(idx["rb_expert"][b])
+        rows = slice(b * 128, (b + 1) * 128)
+        ref = gemm_ref(post_ref[rows], w1[e].cpu())
+        err = rel_fro(out_cpu[rows].float(), ref)
+        assert err < TOL, (int(b), e, err)
+
+
 def test_config5_moe_layer_full(dev):
     """Configs 4/5: 4096 tokens x 7168, top-8 of 256 (Zipf 1.1), 32 local
     experts; the fused-dispatch layer checked on sampled tokens."""

@@ -553,3 +553,54 @@ def test_gemm_ar_graph_replays_device_epoch(dev):
                     num_producers=-1, stage_counters=e_counters, done_flags=e_done)
         torch.cuda.synchronize()
         assert torch.equal(C.cpu(), ref.cpu()), rep
+
+
+def test_grid_larger_than_device_is_refused(dev):
+    """Every workgroup of a persistent launch must be resident (flag waits,
+    cooperative staging and the K-split exchange wait on each other): a grid
+    above the CU count is refused before any launch."""
+    _say("grid > CUs refused")
+    cus = ops.cu_count()
+    A = torch.zeros((256, 256), dtype=torch.bfloat16, device=dev)
+    with pytest.raises(MkError, match="num_cus"):
+        ops.gemm(A, A, num_cus=cus + 8)
+    C = torch.empty_like(A)
+    flags = torch.zeros(2, dtype=torch.int32, device=dev)
+    with pytest.raises(MkError, match="num_cus"):
+        ops.ag_gemm(A, A, A, C, flags, None, epoch=1, num_cus=cus + 1, stage_counters=torch.zeros_like(flags))
+    with pytest.raises(MkError, match="num_cus"):
+        ops.gemm_rs(A, A, C, C, None, None, 1, 0, None, None, epoch=1, gated=False, num_cus=2 * cus)
+    with pytest.raises(MkError, match="num_cus"):
+        ops.gemm_ar(A, A, C, None, None, 1, None, None, epoch=1, gated=False, num_cus=cus + 1)
+    rbe = torch.zeros(2, dtype=torch.int32, device=dev)
+    with pytest.raises(MkError, match="num_cus"):
+        ops.moe_grouped_gemm(A, A.view(1, 256, 256), C, rb_expert=rbe, num_cus=cus + 1)
+    torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("world,rank", [(8, 3), (8, 0)])
+def test_ag_gemm_present_blocks_not_copied(dev, world, rank):
+    """n_present: the first stage positions name blocks already in A_full
+    (the own shard); their flags are published, their source rows are never
+    read (junk there must not reach A_full or C)."""
+    _say(f"ag n_present world={world} rank={rank}")
+    cfg = wl.AgCfg(world=world, shard_rows=256, K=512, N=512)
+    A, B, order = wl.ag_inputs(cfg)
+    nb, per = cfg.M // 128, cfg.shard_rows // 128
+    own = list(range(rank * per, (rank + 1) * per))
+    full_order = torch.tensor(own + [int(b) for b in order if int(b) not in own], dtype=torch.int32, device=dev)
+    src = A.clone()
+    src[rank * cfg.shard_rows:(rank + 1) * cfg.shard_rows] = float("nan")
+    A_full = torch.zeros_like(A)
+    A_full[rank * cfg.shard_rows:(rank + 1) * cfg.shard_rows] = A[rank * cfg.shard_rows:(rank + 1) * cfg.shard_rows]
+    A_full = A_full.to(dev)
+    flags = torch.zeros(nb, dtype=torch.int32, device=dev)
+    counters = torch.zeros_like(flags)
+    C = torch.empty((cfg.M, cfg.N), dtype=torch.bfloat16, device=dev)
+    for epoch, prod in ((1, -1), (2, -2), (3, 4)):
+        ops.ag_gemm(src.to(dev), A_full, B.to(dev), C, flags, full_order, epoch=epoch, num_producers=prod,
+                    stage_counters=counters, n_present=per)
+        torch.cuda.synchronize()
+        assert torch.equal(A_full.cpu(), A)
+        assert (flags.cpu() == epoch).all()
+        assert rel_fro(C.float(), ag_gemm_ref(A, B)) < TOL

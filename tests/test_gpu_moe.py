@@ -135,6 +135,42 @@ def test_invert_slots_bit_exact(dev):
     assert np.array_equal(s2r.cpu().numpy(), idx["slot_to_row"])
 
 
+def test_invert_slots_owner_and_capacity(dev):
+    """Rows of another owner are left out, slots past the capacity are not
+    written and are reported, every other entry ends at -1 (the combine
+    skips those slots)."""
+    _say("moe invert slots owner / capacity")
+    r2s = torch.tensor([3, 0, 7, 1, 2, 9, 0], dtype=torch.int32, device=dev)
+    own = torch.tensor([0, 0, 1, 0, -1, 0, 0], dtype=torch.int32, device=dev)
+    s2r = torch.full((5,), 123, dtype=torch.int32, device=dev)
+    err = torch.zeros(1, dtype=torch.int32, device=dev)
+    ops.moe_invert_slots(r2s[:6], own[:6], s2r, owner=0, error_word=err)
+    torch.cuda.synchronize()
+    # row 2 belongs to owner 1, row 4 is padding, row 5's slot 9 is past the capacity 5
+    assert s2r.cpu().tolist() == [1, 3, -1, 0, -1]
+    assert int(err.item()) == 2
+    err.zero_()
+    ops.moe_invert_slots(r2s[:6], own[:6], s2r, owner=1, error_word=err)
+    torch.cuda.synchronize()
+    assert s2r.cpu().tolist() == [-1, -1, -1, -1, -1] and int(err.item()) == 2  # slot 7 of owner 1 is past it too
+
+
+def test_combine_skips_unproduced_slots(dev):
+    """A slot whose row stays -1 (produced on another GPU) adds nothing."""
+    _say("moe combine skips -1 slots")
+    H = 256
+    ye = wl.randn_bf16((4, H), 3, 1.0).to(dev)
+    w = torch.tensor([0.5, 2.0, 1.0, 3.0], dtype=torch.float32, device=dev)
+    off = torch.tensor([0, 2, 3], dtype=torch.int32, device=dev)
+    s2r = torch.tensor([1, -1, 3], dtype=torch.int32, device=dev)
+    y = torch.full((2, H), 9.0, dtype=torch.float32, device=dev)
+    ops.moe_combine(ye, w, off, s2r, y)
+    torch.cuda.synchronize()
+    yf = ye.float().cpu()
+    assert torch.equal(y.cpu()[0], 2.0 * yf[1])
+    assert torch.equal(y.cpu()[1], 3.0 * yf[3])
+
+
 @pytest.mark.parametrize("tile_n", [0, 256])
 def test_ffn_combine_end_to_end(dev, tile_n):
     _say(f"moe ffn+combine tile_n={tile_n}")
