@@ -116,6 +116,22 @@ typedef struct mk_ag_gemm_args {
 } mk_ag_gemm_args;
 int mk_ag_gemm(const mk_ag_gemm_args* args, void* stream);
 
+/* mk_ag_gemm without any allocation.  No counterpart in the reference: it
+ * is for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  The
+ * K-split workspace and the cooperative-staging piece counters come from a
+ * static device array of mk_ag_gemm_noalloc_scratch_bytes() bytes (about
+ * 32 MB, one copy per GPU, held until the process ends); split_ws,
+ * split_ws_bytes and stage_counters must be NULL / 0.  Limits: M/128 <=
+ * 16384 row blocks (larger M returns MK_ESHAPE); a tail round whose K-split
+ * would need more than 128 partial tiles runs unsplit.  Each call first
+ * clears the counters and split flags it uses on `stream` (a small kernel),
+ * then launches mk_ag_gemm's kernels.  Every call on one GPU shares that
+ * GPU's array: calls that overlap in time on one GPU (different streams)
+ * race and must not be issued. */
+int mk_ag_gemm_noalloc(const mk_ag_gemm_args* args, void* stream);
+int64_t mk_ag_gemm_noalloc_scratch_bytes(void);
+
 /* ------------------------------------------------------------------------ */
 /* GEMM + reduce-scatter epilogue at one rank's share.
  * P = A[M,K] @ B[K,N] (this rank's partial over all M rows).  Rows owned by

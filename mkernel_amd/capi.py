@@ -18,6 +18,8 @@ ABI_VERSION = 6  # include/mk.h mk_abi_version(): the structures below match thi
 EXPORTS = (
     "mk_gemm",
     "mk_ag_gemm",
+    "mk_ag_gemm_noalloc",
+    "mk_ag_gemm_noalloc_scratch_bytes",
     "mk_gemm_rs",
     "mk_gemm_ar",
     "mk_moe_index_sizes",
@@ -136,7 +138,7 @@ def lib() -> C.CDLL:
             raise RuntimeError(f"{LIB_PATH} is missing: run __graft_entry__.build() "
                                "(or python -m mkernel_amd._build) first")
         L = C.CDLL(str(LIB_PATH))
-        for name in ("mk_gemm", "mk_ag_gemm", "mk_gemm_rs", "mk_gemm_ar", "mk_moe_permute", "mk_moe_grouped_gemm",
+        for name in ("mk_gemm", "mk_ag_gemm", "mk_ag_gemm_noalloc", "mk_gemm_rs", "mk_gemm_ar", "mk_moe_permute", "mk_moe_grouped_gemm",
                      "mk_moe_combine", "mk_moe_ffn_combine"):
             getattr(L, name).argtypes = [vp, vp]
             getattr(L, name).restype = C.c_int
@@ -152,6 +154,8 @@ def lib() -> C.CDLL:
         L.mk_moe_invert_slots.restype = C.c_int
         L.mk_moe_tile_rows.argtypes = [vp, i64, vp, vp]
         L.mk_moe_tile_rows.restype = C.c_int
+        L.mk_ag_gemm_noalloc_scratch_bytes.argtypes = []
+        L.mk_ag_gemm_noalloc_scratch_bytes.restype = i64
         L.mk_query_workspace_bytes.argtypes = [i32, i64, i64, i64]
         L.mk_query_workspace_bytes.restype = i64
         L.mk_probe_mfma_ceiling.argtypes = [i64, i32, vp, vp, vp]

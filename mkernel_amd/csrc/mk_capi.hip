@@ -145,6 +145,56 @@ hipError_t launch_build_indices(const int32_t* ids, const float* gates, int T, i
                                 hipStream_t stream);
 }
 
+// ---------------------------------------------------------------------------
+// mk_ag_gemm_noalloc: mk_ag_gemm with its scratch (the K-split workspace and
+// the cooperative-staging piece counters) in `scratch`, a static device
+// array: one copy per GPU, held until the process ends, so the call makes no
+// allocation.  Layout: [K-split flag words, 4 KB][kNoAllocTiles fp32
+// 256x256 partial tiles][kNoAllocCounters piece counters].  Host code never
+// uses the symbol's name as an address: the device address comes from
+// hipGetSymbolAddress, once per device, and only that pointer is passed on.
+// ---------------------------------------------------------------------------
+namespace {
+constexpr int64_t kNoAllocTiles = 128;        // K-split partial tiles (32 MB)
+constexpr int64_t kNoAllocCounters = 16384;   // one per 128-row block: M <= 2^21 rows
+constexpr int64_t kNoAllocSplitBytes = kSplitFlagBytes + kNoAllocTiles * kSplitTileBytes;
+constexpr int64_t kNoAllocBytes = kNoAllocSplitBytes + kNoAllocCounters * 4;
+}  // namespace
+
+static __device__ __align__(256) unsigned char scratch[kNoAllocBytes];
+
+namespace {
+std::mutex g_scratch_mu;
+std::vector<void*> g_scratch_ptr;  // device address of `scratch`, per device
+
+// Device address of this device's `scratch` (looked up on the first call on
+// each device, with that device current).
+int scratch_ptr(void** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if ((int)g_scratch_ptr.size() <= dev) g_scratch_ptr.resize(dev + 1, nullptr);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return hip_fail(e, "hipGetSymbolAddress(scratch)");
+    if (!p) return fail(MK_EDEVICE, "hipGetSymbolAddress(scratch) returned no address");
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return MK_OK;
+}
+
+// Zeroes the K-split flag words and the first n_counters piece counters (a
+// kernel rather than hipMemsetAsync, so the call can be graph-captured).
+__global__ void clear_scratch_kernel(uint32_t* split_flags, int n_flags, uint32_t* counters, int n_counters) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n_flags) split_flags[i] = 0u;
+  if (i < n_counters) counters[i] = 0u;
+}
+}  // namespace
+
 extern "C" {
 
 const char* mk_last_error_string(void) { return g_err.c_str(); }
@@ -282,6 +332,34 @@ int mk_ag_gemm(const mk_ag_gemm_args* a, void* stream) {
   hipError_t e = mk::launch_gemm(p, bm, mk::kEpiStore, static_cast<hipStream_t>(stream));
   return e == hipSuccess ? MK_OK : hip_fail(e, "mk_ag_gemm launch");
 }
+
+int mk_ag_gemm_noalloc(const mk_ag_gemm_args* a, void* stream) {
+  if (!a) return fail(MK_EINVAL, "mk_ag_gemm_noalloc: null argument");
+  if (a->split_ws || a->split_ws_bytes || a->stage_counters)
+    return fail(MK_EINVAL, "mk_ag_gemm_noalloc: split_ws and stage_counters come from the library's static scratch; "
+                           "pass them as NULL / 0");
+  if (a->M < 0 || a->M / 128 > kNoAllocCounters)
+    return fail(MK_ESHAPE, "mk_ag_gemm_noalloc: M=%lld exceeds the static scratch (at most %lld 128-row blocks)",
+                (long long)a->M, (long long)kNoAllocCounters);
+  DevInfo d;
+  if (int rc = device_info(&d)) return rc;
+  void* base = nullptr;
+  if (int rc = scratch_ptr(&base)) return rc;
+  mk_ag_gemm_args b = *a;
+  b.split_ws = base;
+  b.split_ws_bytes = kNoAllocSplitBytes;  // a tail split needing more partial tiles is not made
+  b.stage_counters = reinterpret_cast<uint32_t*>(static_cast<char*>(base) + kNoAllocSplitBytes);
+  const int n_counters = (int)(a->M / 128);
+  const int n_flags = (int)(kSplitFlagBytes / 4);
+  const int n = std::max(n_flags, n_counters);
+  hipLaunchKernelGGL(clear_scratch_kernel, dim3((n + 255) / 256), dim3(256), 0, static_cast<hipStream_t>(stream),
+                     static_cast<uint32_t*>(base), n_flags, b.stage_counters, n_counters);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return hip_fail(e, "mk_ag_gemm_noalloc scratch clear");
+  return mk_ag_gemm(&b, stream);
+}
+
+int64_t mk_ag_gemm_noalloc_scratch_bytes(void) { return kNoAllocBytes; }
 
 int mk_gemm_rs(const mk_gemm_rs_args* a, void* stream) {
   if (!a || !a->A || !a->B || !a->workspace || !a->output) return fail(MK_EINVAL, "mk_gemm_rs: null argument");
