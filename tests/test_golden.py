@@ -77,3 +77,37 @@ def test_moe_fixture_discriminates_silu_sign():
         ye_wrong[r:r + n] = wrong[r:r + n] @ m["w2"][e].float()
         r += n
     assert rel_fro(ye_wrong, torch.from_numpy(F["moe_y_expert"])) > 0.2
+
+
+def test_moe_fixture_pinned_by_scalar_restatement():
+    """The fixture's y_expert / y were written by the oracle; here they are
+    recomputed for a few rows and tokens by a scalar restatement that shares
+    no code with it (expert from the padded ranges, h = x W1[e] in Python
+    doubles, silu(g) = g / (1 + e^-g), y = act
+    W2[e], combine as the gate-weighted sum over the token's routed rows)."""
+    import math
+    m = moe_inputs()
+    pull = F["moe_pull_indices"]
+    padded = F["moe_padded_tokens_per_expert"]
+    bounds = np.cumsum(padded)
+    x = m["tokens"].float().numpy().astype(np.float64)
+    W1 = m["w1"].float().numpy().astype(np.float64)
+    W2 = m["w2"].float().numpy().astype(np.float64)
+    I = m["I"]
+
+    def row_y(r):
+        e = int(np.searchsorted(bounds, r, side="right"))
+        xr = x[int(pull[r, 2])]
+        h = [float(sum(xr[k] * W1[e, k, j] for k in range(xr.shape[0]))) for j in range(2 * I)]
+        act = [h[j] / (1.0 + math.exp(-h[j])) * h[I + j] for j in range(I)]
+        return np.array([sum(act[j] * W2[e, j, c] for j in range(I)) for c in range(W2.shape[2])])
+
+    ye = F["moe_y_expert"]
+    for r in (0, 5, 128, 133):   # two rows of each local expert
+        assert np.allclose(row_y(r), ye[r], rtol=1e-4, atol=1e-4), r
+    w = F["moe_row_weight"]
+    for t in (0, 2):             # token 0: one local expert; token 2: both
+        rows = [r for r in range(pull.shape[0]) if pull[r, 0] >= 0 and pull[r, 2] == t]
+        assert len(rows) == (1 if t == 0 else 2)
+        y = sum(float(w[r]) * row_y(r) for r in rows)
+        assert np.allclose(y, F["moe_y"][t], rtol=1e-4, atol=1e-4), t

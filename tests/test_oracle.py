@@ -10,6 +10,7 @@ import torch
 from mkernel_amd import workloads as wl
 from oracle import gemm as og
 from oracle import moe as om
+from oracle.gemm import gemm_ref, rel_fro
 from oracle.cmoe import build_indices_c
 
 GOLDEN = Path(__file__).resolve().parent / "golden"
@@ -191,3 +192,63 @@ def test_gemm_ar_ref_known_answers():
     a = torch.tensor([[1.0, 2.0]]).bfloat16(); b = torch.tensor([[3.0], [4.0]]).bfloat16()
     peers = torch.tensor([[[0.5]], [[-2.0]]]).bfloat16()
     assert gemm_ar_ref(a, b, peers).item() == 11.0 + 0.5 - 2.0
+
+
+def test_grouped_gemm_ref_single_expert_is_gemm():
+    """One expert covering every row: the grouped GEMM is the plain GEMM."""
+    post = wl.randn_bf16((256, 64), 40, 1.0)
+    w = wl.randn_bf16((1, 64, 48), 41, 0.125)
+    assert torch.equal(om.grouped_gemm_ref(post, w, [256]), gemm_ref(post, w[0]))
+
+
+def test_grouped_gemm_ref_selects_each_experts_weights():
+    """Expert-tagged weights: W[e] = (e + 1) * I (square), so row r comes out
+    as (e(r) + 1) * post[r] exactly — a block routed to the wrong expert, an
+    off-by-one expert boundary or a dropped empty expert shows up as a wrong
+    multiple.  Experts with zero padded rows are skipped without shifting
+    the row ranges of the next ones."""
+    H = 16
+    padded = [128, 0, 256, 128, 0]
+    post = wl.randn_bf16((sum(padded), H), 42, 1.0)
+    w = torch.stack([(e + 1) * torch.eye(H) for e in range(len(padded))]).to(torch.bfloat16)
+    out = om.grouped_gemm_ref(post, w, padded)
+    mult = torch.tensor(sum([[e + 1] * n for e, n in enumerate(padded)], []), dtype=torch.float32)
+    assert torch.equal(out, post.float() * mult[:, None])
+
+
+def _ffn_bruteforce(post, w1, w2, padded, I):
+    """Per row, per output column, in Python doubles: expert from the padded
+    ranges, h = x @ W1[e], act = silu(h[:I]) * h[I:], y = act @ W2[e]."""
+    import math
+    x = post.float().tolist()
+    W1 = w1.float().tolist()
+    W2 = w2.float().tolist()
+    bounds = np.cumsum(padded)
+    acts, ys = [], []
+    for r, xr in enumerate(x):
+        e = int(np.searchsorted(bounds, r, side="right"))
+        h = [sum(xr[k] * W1[e][k][j] for k in range(len(xr))) for j in range(2 * I)]
+        a = [h[j] / (1.0 + math.exp(-h[j])) * h[I + j] for j in range(I)]
+        acts.append(a)
+        ys.append([sum(a[j] * W2[e][j][c] for j in range(I)) for c in range(len(W2[e][0]))])
+    return torch.tensor(acts, dtype=torch.float64), torch.tensor(ys, dtype=torch.float64)
+
+
+def test_ffn_ref_matches_bruteforce():
+    """ffn_ref against a scalar restatement on a tiny two-expert case whose
+    pre-activations are O(1) (silu far from linear), both halves of W1
+    distinct: a swapped gate/up half, a sign slip in the exponential or the
+    wrong expert's W2 misses by far more than the tolerance."""
+    H, I = 12, 5
+    padded = [3, 0, 4]
+    post = wl.randn_bf16((7, H), 43, 1.0)
+    w1 = wl.randn_bf16((3, H, 2 * I), 44, 0.6)
+    w2 = wl.randn_bf16((3, I, H), 45, 0.6)
+    act, y = om.ffn_ref(post, w1, w2, padded, I)
+    act_b, y_b = _ffn_bruteforce(post, w1, w2, padded, I)
+    assert torch.allclose(act.double(), act_b, rtol=1e-5, atol=1e-5)
+    assert torch.allclose(y.double(), y_b, rtol=1e-5, atol=1e-5)
+    # the same inputs with the gate and up halves swapped differ markedly
+    w1s = torch.cat([w1[:, :, I:], w1[:, :, :I]], 2)
+    _, y_s = om.ffn_ref(post, w1s, w2, padded, I)
+    assert rel_fro(y_s, y_b) > 0.2
