@@ -44,10 +44,17 @@ class Timer:
         self.s = torch.cuda.Event(enable_timing=True)
         self.e = torch.cuda.Event(enable_timing=True)
 
-    def run(self, fn, steps: int, warmup: int) -> float:
+    def run(self, fn, steps: int, warmup: int, primed: bool = False) -> float:
+        """Mean ms per step of `steps` launches.  primed=False: synchronize
+        after the warmup, so the timed region starts with an empty queue and
+        the first launch's host latency is inside it (the contract's
+        synchronize-bracketed step).  primed=True: the start event is queued
+        behind the warmup launches, so the region holds back-to-back launches
+        only (steady state, comparable with a profiler's kernel average)."""
         for i in range(warmup):
             fn(i)
-        torch.cuda.synchronize()
+        if not primed:
+            torch.cuda.synchronize()
         self.s.record()
         for i in range(steps):
             fn(warmup + i)
@@ -121,7 +128,12 @@ def bench_gemm(steps, warmup, extra):
     C = torch.empty((cfg.M, cfg.N), dtype=torch.bfloat16, device="cuda")
     flops = 2.0 * cfg.M * cfg.N * cfg.K
     ms = Timer().run(lambda i: ops.gemm(A, B, C), steps, warmup)
-    extra["gemm_4096"] = {"us": ms * 1e3, "tflops": flops / ms / 1e9, "frac_peak": flops / ms / 1e9 / PEAK_BF16_TFLOPS}
+    # the same launches with the queue kept full: a profiler's per-kernel
+    # average excludes the empty-queue start (one host launch latency) that
+    # a synchronize-bracketed region of a ~0.1 ms kernel includes
+    ms_primed = Timer().run(lambda i: ops.gemm(A, B, C), max(steps, 50), max(warmup, 5), primed=True)
+    extra["gemm_4096"] = {"us": ms * 1e3, "tflops": flops / ms / 1e9, "frac_peak": flops / ms / 1e9 / PEAK_BF16_TFLOPS,
+                          "us_back_to_back": ms_primed * 1e3, "tflops_back_to_back": flops / ms_primed / 1e9}
 
 
 def bench_rs(steps, warmup, producers, extra):
@@ -185,6 +197,7 @@ def moe_setup(cfg: wl.MoeCfg):
 
 
 def bench_moe(steps, warmup, extra):
+    """Configs 4 and 5; returns the layer's inputs (for the CPU baseline)."""
     cfg = wl.MoeCfg()
     tokens, w1, w2, idx, d = moe_setup(cfg)
     R, R_pad = idx["R"], idx["R_pad"]
@@ -275,6 +288,18 @@ def bench_moe(steps, warmup, extra):
                                 "hbm_bound_GBs": layer_bytes / ms5 / 1e6,
                                 "us_gemm1_swiglu": ms_g1 * 1e3, "us_gemm2": ms_g2 * 1e3, "us_combine": ms_comb * 1e3,
                                 "weight_bytes": w_bytes1 + w_bytes2}
+    # HBM roofline of the layer: every used expert's W1 and W2 streamed once
+    # is the floor; at R routed rows the layer's intensity (FLOP per byte of
+    # that traffic) caps the MFMA fraction far below the published peak
+    intensity = f5 / layer_bytes
+    ridge = PEAK_BF16_TFLOPS * 1e12 / (PEAK_HBM_GBS * 1e9)
+    extra["moe_ffn_combine"]["roofline"] = {
+        "bound": "hbm", "achieved": (w_bytes1 + w_bytes2) / ms5 / 1e6, "peak": PEAK_HBM_GBS, "unit": "GB/s",
+        "frac": (w_bytes1 + w_bytes2) / ms5 / 1e6 / PEAK_HBM_GBS, "basis": "unique expert weight bytes per layer",
+        "intensity_flop_per_byte": intensity, "ridge_flop_per_byte": ridge,
+        "mfma_frac_cap_at_this_intensity": intensity / ridge,
+        "note": "the layer streams 2.8 GB of weights for 6*R*H*I FLOP: at this intensity no kernel can exceed "
+                "mfma_frac_cap_at_this_intensity of the bf16 MFMA peak, so the HBM fraction is the bar"}
     extra["moe_index_build"] = {"us_gpu": ms_idx * 1e3, "us_host_cpp_1thread": ms_idx_host * 1e3,
                                 "entries": cfg.tokens * cfg.topk}
     extra["moe_routed_layer_device_count"] = {
@@ -282,9 +307,55 @@ def bench_moe(steps, warmup, extra):
                 "device (buffers at capacity, no host read-back)",
         "us_eager": r_routed["eager"] * 1e3, "us_graph_replay": r_routed["graph"] * 1e3,
         "tokens_per_s_graph": cfg.tokens / r_routed["graph"] * 1e3, "capacity_rows": cap}
+    return tokens, ids_np, gates_np, w1, w2
 
 
 # ------------------------------------------------------------ CPU baseline
+def cpu_baseline_moe(inputs, tokens_per_sample: int = 1024, reps: int = 3) -> dict:
+    """Config 5's layer in float32 torch on the host cores, on a bounded
+    sample: the first `tokens_per_sample` tokens of the same routing, their
+    routed rows gathered with index_select, per-expert matmul, F.silu(g) * u,
+    matmul, gate-weighted index_add_ back to token order.  Tokens/s of the
+    sample (the work scales with the routed rows)."""
+    import torch.nn.functional as F
+    cfg = wl.MoeCfg()
+    tokens, ids, gates, w1, w2 = (t.cpu() if torch.is_tensor(t) else t for t in inputs)  # the GPU run's inputs
+    T = tokens_per_sample
+    idx = ops.moe_build_indices(ids[:T], gates[:T], cfg.e0, cfg.n_local)
+    pull = torch.from_numpy(idx["pull_indices"]).long()
+    real = pull[:, 0] >= 0
+    src = pull[real, 2]
+    wts = torch.from_numpy(idx["row_weight"])[real]
+    expert = torch.from_numpy(idx["row_expert"]).long()[real]
+    x = tokens[:T].float()
+    w1f, w2f = w1.float(), w2.float()
+    torch.set_num_threads(os.cpu_count() or 1)
+
+    def layer():
+        rows = x.index_select(0, src)
+        y = torch.zeros((T, cfg.H), dtype=torch.float32)
+        for e in torch.unique(expert).tolist():
+            sel = torch.nonzero(expert == e).flatten()
+            h = rows.index_select(0, sel) @ w1f[e]
+            a = F.silu(h[:, :cfg.I]) * h[:, cfg.I:]
+            ye = a @ w2f[e]
+            y.index_add_(0, src.index_select(0, sel), wts.index_select(0, sel)[:, None] * ye)
+        return y
+
+    layer()
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        layer()
+        times.append(time.perf_counter() - t0)
+    t = statistics.median(times)
+    return {"value": T / t, "unit": "tokens/s", "cores": torch.get_num_threads(), "cpu_count": os.cpu_count(),
+            "kind": "port",
+            "sample": f"first {T} of 4096 tokens ({int(real.sum())} routed rows), fp32 torch on CPU: index_select, "
+                      f"per-expert matmul, F.silu(g)*u, matmul, weighted index_add_; median of {reps}",
+            "seconds": t}
+
+
 def cpu_baseline(A_full, B, rows: int = 256, reps: int = 3):
     """The oracle's float32 torch matmul on the host cores, on a bounded
     sample of the same workload: `rows` rows of A_full times B."""
@@ -304,14 +375,18 @@ def cpu_baseline(A_full, B, rows: int = 256, reps: int = 3):
 
 
 def load_traffic():
-    """HBM bytes per launch measured with rocprofv3 --pmc (FETCH_SIZE +
-    WRITE_SIZE, scaled by the copy-kernel calibration), if recorded."""
+    """(bytes, source) of the headline kernel's HBM traffic per launch, read
+    from profiles/traffic.json (rocprofv3 --pmc FETCH_SIZE + WRITE_SIZE,
+    scaled by the copy-kernel calibration; not measured in this run: the
+    counters need their own profiler runs), or (None, None)."""
     path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "traffic.json")
     try:
         with open(path) as f:
-            return json.load(f).get("ag_gemm_gated_bytes_per_launch")
+            t = json.load(f)
     except (OSError, ValueError):
-        return None
+        return None, None
+    src = "profiles/traffic.json: " + t.get("source", "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs")
+    return t.get("ag_gemm_gated_bytes_per_launch"), src
 
 
 def main():
@@ -340,6 +415,7 @@ def main():
         log("[bench] ag_gemm config 2")
         ms, flops, (A_full, B) = bench_ag(K, W, args.producers, extra)
         tflops = flops / ms / 1e9
+        traffic, traffic_src = load_traffic()
         line = {
             "metric": METRIC, "value": round(tflops, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": K, "warmup": W,
             "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
@@ -348,7 +424,8 @@ def main():
                                    "B 8192x3584, C 16384x3584, 128-row flags, staged in-launch (producer role)",
                        "M": 16384, "N": 3584, "K": 8192, "producers": args.producers, "parallelism": "tp8-rank-share"},
             "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                         "frac": round(tflops / PEAK_BF16_TFLOPS, 4), "traffic": load_traffic()},
+                         "frac": round(tflops / PEAK_BF16_TFLOPS, 4), "traffic": traffic,
+                         "traffic_source": traffic_src},
         }
         if not args.no_cpu:
             log("[bench] cpu baseline")
@@ -368,7 +445,12 @@ def main():
         torch.cuda.empty_cache()
     if args.workload in ("all", "moe"):
         log("[bench] moe configs 4/5")
-        bench_moe(K, W, extra)
+        moe_in = bench_moe(K, W, extra)
+        if not args.no_cpu:
+            log("[bench] moe cpu baseline")
+            extra["moe_ffn_combine"]["cpu_baseline"] = cpu_baseline_moe(moe_in)
+        del moe_in
+        torch.cuda.empty_cache()
     if args.workload in ("all", "ceiling"):
         # What the matrix cores sustain on this board (power-limited clock),
         # next to the published peak the roofline is priced against.
@@ -391,8 +473,14 @@ def main():
                                      "GBs": 2 * rows * H * 2 / ms / 1e6}
     if line is None:
         line = {"metric": METRIC, "value": None, "unit": "TFLOP/s", "n_gpus": 1, "steps": K, "warmup": W}
-    line["extra"] = {k: {kk: (round(vv, 4) if isinstance(vv, float) else vv) for kk, vv in v.items()}
-                     for k, v in extra.items()}
+    def rnd(v):
+        if isinstance(v, float):
+            return round(v, 4)
+        if isinstance(v, dict):
+            return {k: rnd(x) for k, x in v.items()}
+        return v
+
+    line["extra"] = rnd(extra)
     print(json.dumps(line), flush=True)
 
 
