@@ -54,8 +54,13 @@ struct Cfg {
   static constexpr uint32_t B_BYTES = BKD * BROW;           // 32 k-rows
   static constexpr int B_UPR = BN / 8;                      // 16-byte units per B k-row
   static constexpr uint32_t STAGE = A_BYTES + B_BYTES;
-  // ring depth: as deep as the 160 KB LDS allows next to the static tables
-  static constexpr int S = (BN == 512) ? 3 : (BM == 256) ? 4 : 6;
+  // Schedule tables in static LDS (arrival-ordered tile order, cooperative
+  // staging): only the 256-row kernels (AllGather / reduce-scatter /
+  // all-reduce) use them; the 128-row expert kernels give the LDS to the ring.
+  static constexpr bool kSched = (BM == 256);
+  // ring depth: as deep as the 160 KB LDS allows (next to the static tables
+  // where there are any): 4 x 40 KB for the 128 x 512 expert tiles
+  static constexpr int S = (BN == 512) ? 4 : (BM == 256) ? 4 : 6;
   static constexpr uint32_t LDS_BYTES = S * STAGE;
   static constexpr int A_INST = A_BYTES / 1024 / WAVES_;    // DMA instructions per wave per stage
   static constexpr int B_INST = B_BYTES / 1024 / WAVES_;
@@ -1191,10 +1196,6 @@ template <int BM, int WAVES, int EPI, int BN>
 __global__ __launch_bounds__(64 * WAVES, 1) void gemm_kernel(GemmKParams p) {
   using C = Cfg<BM, WAVES, BN>;
   extern __shared__ __attribute__((aligned(16))) char smem[];
-  __shared__ int row_perm[kMaxTilesM];
-  __shared__ uint16_t full_list[kMaxSplitListTiles];
-  __shared__ int row_key[kMaxTilesM];
-  __shared__ int round_need[kMaxRounds];
   if ((int)blockIdx.x < p.n_prod) {
     producer_role<C::NT>(p, blockIdx.x);
     return;
@@ -1204,43 +1205,55 @@ __global__ __launch_bounds__(64 * WAVES, 1) void gemm_kernel(GemmKParams p) {
   // so give each XCD a contiguous run of consumer ids (hence of tiles, which
   // the grouped order keeps close in A rows / B columns) for L2 reuse.
   if (p.xcd_remap) cons = (cons % 8) * (p.n_cons / 8) + cons / 8;
-  const int* perm = nullptr;
-  if (p.perm_mode != kPermNone) {
-    build_row_perm<BM, C::NT>(p, row_perm, row_key, reinterpret_cast<int*>(smem));
-    perm = row_perm;
-  }
-  const uint16_t* flist = nullptr;
-  if (perm && p.sk_split > 1) {
-    build_full_list<C::NT>(p, row_perm, full_list, reinterpret_cast<int*>(smem));
-    flist = full_list;
-  }
-  // Cooperative staging runs between tile rounds when the schedule's
-  // staging needs are known (a permuted order with at most kMaxRounds
-  // rounds); otherwise all of it runs before the first tile.
   StagePlan sp;
   sp.q = cons;
   sp.batch = 1;
   sp.n_rounds = 0;
   sp.round_need = nullptr;
   sp.grp = sp.gid = sp.gsize = 0;
-  if (p.st_coop) {
-    const int ntiles = p.tiles_m * p.tiles_n;
-    const int full = (p.sk_split > 1) ? p.sk_full : ntiles;
-    const int n_rounds = (full + p.n_cons - 1) / p.n_cons;
-    if (perm && n_rounds <= kMaxRounds) {
-      build_round_need<C::NT>(p, full, n_rounds, flist, row_key, round_need);
-      sp.n_rounds = n_rounds;
-      sp.round_need = round_need;
-      if (p.st_coop == 2 && p.xcd_remap && n_rounds >= 1) {
-        sp.gsize = p.n_cons / 2;
-        sp.grp = cons / sp.gsize;
-        sp.gid = cons % sp.gsize;
-      }
-    } else {
-      coop_stage<C::NT>(p, p.n_cons, sp.q, sp.batch, p.st_nblocks * kPieces);
+  if constexpr (C::kSched) {
+    __shared__ int row_perm[kMaxTilesM];
+    __shared__ uint16_t full_list[kMaxSplitListTiles];
+    __shared__ int row_key[kMaxTilesM];
+    __shared__ int round_need[kMaxRounds];
+    const int* perm = nullptr;
+    if (p.perm_mode != kPermNone) {
+      build_row_perm<BM, C::NT>(p, row_perm, row_key, reinterpret_cast<int*>(smem));
+      perm = row_perm;
     }
+    const uint16_t* flist = nullptr;
+    if (perm && p.sk_split > 1) {
+      build_full_list<C::NT>(p, row_perm, full_list, reinterpret_cast<int*>(smem));
+      flist = full_list;
+    }
+    // Cooperative staging runs between tile rounds when the schedule's
+    // staging needs are known (a permuted order with at most kMaxRounds
+    // rounds); otherwise all of it runs before the first tile.
+    if (p.st_coop) {
+      const int ntiles = p.tiles_m * p.tiles_n;
+      const int full = (p.sk_split > 1) ? p.sk_full : ntiles;
+      const int n_rounds = (full + p.n_cons - 1) / p.n_cons;
+      if (perm && n_rounds <= kMaxRounds) {
+        build_round_need<C::NT>(p, full, n_rounds, flist, row_key, round_need);
+        sp.n_rounds = n_rounds;
+        sp.round_need = round_need;
+        if (p.st_coop == 2 && p.xcd_remap && n_rounds >= 1) {
+          sp.gsize = p.n_cons / 2;
+          sp.grp = cons / sp.gsize;
+          sp.gid = cons % sp.gsize;
+        }
+      } else {
+        coop_stage<C::NT>(p, p.n_cons, sp.q, sp.batch, p.st_nblocks * kPieces);
+      }
+    }
+    compute_role<C, EPI>(p, cons, smem, perm, flist, sp);
+  } else {
+    // 128-row kernels: no arrival order and no staging (the host never
+    // launches them with either); cooperative staging, if asked for, runs
+    // before the first tile.
+    if (p.st_coop) coop_stage<C::NT>(p, p.n_cons, sp.q, sp.batch, p.st_nblocks * kPieces);
+    compute_role<C, EPI>(p, cons, smem, nullptr, nullptr, sp);
   }
-  compute_role<C, EPI>(p, cons, smem, perm, flist, sp);
 }
 
 // One thread: *epoch_ptr + 1, skipping 0 (a vector store, ordered before
