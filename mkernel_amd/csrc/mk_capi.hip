@@ -672,6 +672,7 @@ static int grouped_gemm_impl(const void* A, const void* W, void* out, const int3
     // plans the tail split itself, which may use up to one partial tile per
     // consumer (and one flag word each).
     p.rows_dev = sizes + 1;
+    p.spread_dev = num_cus <= 0 ? 1 : 0;  // the library's grid: the kernel applies the tail spread
     if (split_ws && p.waves == 8 && (int64_t)p.n_cons * 4 <= kSplitFlagBytes &&
         split_ws_bytes >= kSplitFlagBytes + (int64_t)p.n_cons * 128 * bn * 4) {
       p.sk_dev = 1;

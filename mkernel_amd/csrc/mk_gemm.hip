@@ -625,8 +625,8 @@ __device__ __forceinline__ void add_partial_regs(const float* src, f32x16 (&acc)
 // epilogue.  Every round then keeps all consumers busy.
 // ---------------------------------------------------------------------------
 template <class C, int EPI>
-__device__ __forceinline__ void compute_role(const GemmKParams& p, int cons_id, char* smem, const int* row_perm,
-                             const uint16_t* full_list, StagePlan& sp) {
+__device__ __forceinline__ void compute_role(const GemmKParams& p, int cons_id, int n_cons, char* smem,
+                                             const int* row_perm, const uint16_t* full_list, StagePlan& sp) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
@@ -644,9 +644,9 @@ __device__ __forceinline__ void compute_role(const GemmKParams& p, int cons_id, 
       const int nt = tiles_m * p.tiles_n;
       sk_split = 0;
       sk_full = nt;
-      const int R = nt % p.n_cons;
+      const int R = nt % n_cons;
       if (p.sk_dev && R != 0) {
-        const int s = min(min(4, p.n_cons / R), (p.K / 32) / 4);
+        const int s = min(min(4, n_cons / R), (p.K / 32) / 4);
         if (s >= 2) {
           sk_split = s;
           sk_full = nt - R;
@@ -682,7 +682,7 @@ __device__ __forceinline__ void compute_role(const GemmKParams& p, int cons_id, 
 
   const int full = (sk_split > 1) ? sk_full : ntiles;
   const int n_tail_units = (ntiles - full) * (sk_split > 1 ? sk_split : 0);
-  const int n_full_mine = (full > cons_id) ? (full - cons_id + p.n_cons - 1) / p.n_cons : 0;
+  const int n_full_mine = (full > cons_id) ? (full - cons_id + n_cons - 1) / n_cons : 0;
 
   // One output tile (or one K range of it): accumulate A[rows] @ B[:, cols]
   // over K stages k0 .. k0+nk into acc.  Called from two places (whole
@@ -1000,16 +1000,16 @@ __device__ __forceinline__ void compute_role(const GemmKParams& p, int cons_id, 
       // an even share of the rest
       const int need = (sp.round_need[w] + 1) * kPieces;
       const int even = (int)((int64_t)st_total * (w + 1) / sp.n_rounds);
-      coop_stage<C::NT>(p, p.n_cons, sp.q, sp.batch, max(need, even));
+      coop_stage<C::NT>(p, n_cons, sp.q, sp.batch, max(need, even));
     }
-    int t = cons_id + w * p.n_cons;
+    int t = cons_id + w * n_cons;
     if (full_list) t = full_list[t];
     f32x16 acc[C::FM][C::FN];
     int m0, tn;
     tile_body(t, row_perm != nullptr, 0, nk_all, acc, m0, tn);
     store_tile<C, EPI>(p, acc, m0, tn, tid, smem);
   }
-  if (sp.round_need && sp.gsize == 0) coop_stage<C::NT>(p, p.n_cons, sp.q, sp.batch, st_total);
+  if (sp.round_need && sp.gsize == 0) coop_stage<C::NT>(p, n_cons, sp.q, sp.batch, st_total);
   // alternating mode: a consumer with no tile in the last whole round
   // still copies its shares of the ranges staged before that round
   if (sp.round_need && sp.gsize > 0)
@@ -1201,10 +1201,32 @@ __global__ __launch_bounds__(64 * WAVES, 1) void gemm_kernel(GemmKParams p) {
     return;
   }
   int cons = blockIdx.x - p.n_prod;
+  int n_cons = p.n_cons;
+  if constexpr (BM == 128) {
+    // Device row count with the library's grid: when the tail round cannot
+    // be K-split (more tail tiles than half the grid), every consumer runs
+    // the same number of whole-tile rounds anyway, so spread the tiles over
+    // the fewest consumers (a multiple of 8) that keep that round count —
+    // the host's rule for host-sized launches; the others exit here.
+    if (p.rows_dev && p.spread_dev) {
+      const int64_t rows = *p.rows_dev;
+      const int nt = (int)min<int64_t>(p.tiles_m, max<int64_t>(rows, 0) / C::BM) * p.tiles_n;
+      const int R = nt % n_cons;
+      if (R != 0 && 2 * R > n_cons) {
+        const int rounds = (nt + n_cons - 1) / n_cons;
+        const int even = ((nt + rounds - 1) / rounds + 7) / 8 * 8;
+        if (even < n_cons) {
+          if (cons >= even) return;
+          n_cons = even;
+        }
+      }
+      n_cons = __builtin_amdgcn_readfirstlane(n_cons);
+    }
+  }
   // XCD-aware renumbering: workgroups are dealt round-robin to the 8 XCDs,
   // so give each XCD a contiguous run of consumer ids (hence of tiles, which
   // the grouped order keeps close in A rows / B columns) for L2 reuse.
-  if (p.xcd_remap) cons = (cons % 8) * (p.n_cons / 8) + cons / 8;
+  if (p.xcd_remap) cons = (cons % 8) * (n_cons / 8) + cons / 8;
   StagePlan sp;
   sp.q = cons;
   sp.batch = 1;
@@ -1246,13 +1268,13 @@ __global__ __launch_bounds__(64 * WAVES, 1) void gemm_kernel(GemmKParams p) {
         coop_stage<C::NT>(p, p.n_cons, sp.q, sp.batch, p.st_nblocks * kPieces);
       }
     }
-    compute_role<C, EPI>(p, cons, smem, perm, flist, sp);
+    compute_role<C, EPI>(p, cons, p.n_cons, smem, perm, flist, sp);
   } else {
     // 128-row kernels: no arrival order and no staging (the host never
     // launches them with either); cooperative staging, if asked for, runs
     // before the first tile.
     if (p.st_coop) coop_stage<C::NT>(p, p.n_cons, sp.q, sp.batch, p.st_nblocks * kPieces);
-    compute_role<C, EPI>(p, cons, smem, nullptr, nullptr, sp);
+    compute_role<C, EPI>(p, cons, n_cons, smem, nullptr, nullptr, sp);
   }
 }
 

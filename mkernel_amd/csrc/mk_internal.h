@@ -71,6 +71,7 @@ struct GemmKParams {
   // then hold n_cons partial tiles).
   const int64_t* rows_dev;
   int sk_dev;
+  int spread_dev;           // with rows_dev: spread an unsplittable tail over fewer consumers (host rule)
   // flag protocol: the epoch is *epoch_ptr when that is set (read once per
   // use at run time, written by an earlier launch), else `epoch`
   const uint32_t* epoch_ptr;
