@@ -210,7 +210,7 @@ __device__ __forceinline__ void wait_lgkm_all() { __builtin_amdgcn_s_waitcnt(0xC
 // WTN*2-byte row segments.  The region is the wave's own, so only this
 // wave's LDS ordering matters (lgkmcnt waits); the caller's workgroup
 // barrier must precede the next use of the ring.
-template <class C, int NJ = C::FN>
+template <class C, int NJ = C::FN, bool NT = false>
 __device__ __forceinline__ void store_rows(uint16_t* base, int64_t ldc, f32x16 (&acc)[C::FM][C::FN], char* smem,
                                            int wave, int lane) {
   constexpr int W = NJ * 32;              // columns stored per row: accumulator blocks j < NJ
@@ -242,7 +242,13 @@ __device__ __forceinline__ void store_rows(uint16_t* base, int64_t ldc, f32x16 (
     for (int r = 0; r < 32 / RPI; ++r) {
       const int row = r * RPI + rr;
       const uint4 v = *reinterpret_cast<const uint4*>(reg + row * PITCH + cc * 16);
-      *reinterpret_cast<uint4*>(base + (int64_t)(i * 32 + row) * ldc + cc * 8) = v;
+      uint4* dst = reinterpret_cast<uint4*>(base + (int64_t)(i * 32 + row) * ldc + cc * 8);
+      if constexpr (NT) {
+        typedef uint32_t nt_u32x4 __attribute__((ext_vector_type(4)));
+        __builtin_nontemporal_store(nt_u32x4{v.x, v.y, v.z, v.w}, reinterpret_cast<nt_u32x4*>(dst));
+      } else {
+        *dst = v;
+      }
     }
     wait_lgkm_all();  // this block's reads are done before the next block's writes
   }
@@ -336,7 +342,11 @@ __device__ __forceinline__ void store_tile(const GemmKParams& p, f32x16 (&acc)[C
   const int wm = wave / C::WN, wn = wave % C::WN;
   const int ml = lane & 31, kg = lane >> 5;
   if constexpr (EPI == kEpiStore) {
-    store_rows<C>(p.C + (int64_t)(m0 + wm * C::WTM) * p.ldc + tn * C::BN + wn * C::WTN, p.ldc, acc, smem, wave, lane);
+    // the 128-row expert tiles write rows read by a later kernel (GEMM2's
+    // y_expert by the combine): nontemporal stores, which measured faster
+    // for both (config 5: GEMM2 224 -> 211 us, layer -6 us)
+    store_rows<C, C::FN, C::BM == 128>(p.C + (int64_t)(m0 + wm * C::WTM) * p.ldc + tn * C::BN + wn * C::WTN, p.ldc,
+                                       acc, smem, wave, lane);
     __syncthreads();  // every wave's LDS reads done before the ring is reused
   } else if constexpr (EPI == kEpiSwiGLU) {
     // silu(g) * u in fp32 with silu(g) = g / (1 + e^-g), as the reference
@@ -352,7 +362,8 @@ __device__ __forceinline__ void store_tile(const GemmKParams& p, f32x16 (&acc)[C
           const float g = acc[i][j][v];
           acc[i][j][v] = (g / (1.0f + __expf(-g))) * acc[i][j + C::FN / 2][v];
         }
-    store_rows<C, C::FN / 2>(p.C + (int64_t)(m0 + wm * C::WTM) * p.ldc + tn * (C::BN / 2) + wn * (C::WTN / 2), p.ldc,
+    store_rows<C, C::FN / 2, true>(p.C + (int64_t)(m0 + wm * C::WTM) * p.ldc + tn * (C::BN / 2) + wn * (C::WTN / 2),
+                                   p.ldc,
                              acc, smem, wave, lane);
     __syncthreads();  // every wave's LDS reads done before the ring is reused
   } else {  // kEpiReduce

@@ -87,17 +87,20 @@ __global__ __launch_bounds__(kThreads) void combine_kernel(CombineKParams p) {
         add(p.row_weight[row], *reinterpret_cast<const uint4*>(p.y_expert + (int64_t)row * p.H + c * 8));
       }
     }
+    // the layer's output is not read again here: nontemporal stores
+    // (config 5 layer -7 us against plain stores)
     if (p.out_dtype == 0) {
       float4* o = reinterpret_cast<float4*>(static_cast<float*>(p.y_out) + t * p.H + c * 8);
-      o[0] = make_float4(acc[0], acc[1], acc[2], acc[3]);
-      o[1] = make_float4(acc[4], acc[5], acc[6], acc[7]);
+      __builtin_nontemporal_store(f32x4{acc[0], acc[1], acc[2], acc[3]}, reinterpret_cast<f32x4*>(o));
+      __builtin_nontemporal_store(f32x4{acc[4], acc[5], acc[6], acc[7]}, reinterpret_cast<f32x4*>(o) + 1);
     } else {
       uint4 w;
       w.x = pack_bf16x2(acc[0], acc[1]);
       w.y = pack_bf16x2(acc[2], acc[3]);
       w.z = pack_bf16x2(acc[4], acc[5]);
       w.w = pack_bf16x2(acc[6], acc[7]);
-      *reinterpret_cast<uint4*>(static_cast<uint16_t*>(p.y_out) + t * p.H + c * 8) = w;
+      typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+      __builtin_nontemporal_store(u4{w.x, w.y, w.z, w.w}, reinterpret_cast<u4*>(static_cast<uint16_t*>(p.y_out) + t * p.H + c * 8));
     }
   }
 }
