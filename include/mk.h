@@ -257,6 +257,7 @@ int mk_moe_build_indices(const int32_t* topk_ids, const float* topk_gates,
  * capacity_rows, sizes still reports it and rows past the capacity are not
  * written (capacity_rows = num_tokens * topk + n_local * (row_block - 1)
  * always suffices).  `workspace` holds mk_moe_index_workspace_bytes bytes.
+ * At most 4096 local experts.
  * No counterpart in the reference, whose builders are host Python
  * (bench/dispatch_gemm_bench.py:127-188,
  * bench/dispatch_gemm_glu_combine_bench.py:222-293, 511-527). */

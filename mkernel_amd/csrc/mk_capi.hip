@@ -747,6 +747,8 @@ int mk_moe_build_indices_dev(const mk_moe_index_dev_args* a, void* stream) {
   if ((int64_t)a->num_tokens * a->topk + (int64_t)a->n_local * a->row_block > (1LL << 31))
     return fail(MK_ESHAPE, "mk_moe_build_indices_dev: too many rows for 32-bit row indices");
   if (a->capacity_rows < 0) return fail(MK_EINVAL, "mk_moe_build_indices_dev: capacity_rows < 0");
+  if (a->n_local > 4096)
+    return fail(MK_ESHAPE, "mk_moe_build_indices_dev: at most 4096 local experts (per-wave expert counts live in LDS)");
   if (!a->workspace || a->workspace_bytes < mk::index_workspace_bytes(a->num_tokens, a->topk, a->n_local))
     return fail(MK_EINVAL, "mk_moe_build_indices_dev: workspace smaller than mk_moe_index_workspace_bytes");
   DevInfo d;

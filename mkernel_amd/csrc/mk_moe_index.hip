@@ -16,12 +16,14 @@
 //
 // Kernels (one stream, in order):
 //   count   per 256-entry chunk, per-expert counts            -> hist[e][chunk]
+//           per 256 tokens, routed entries                     -> tok[t]
 //   plan    one block: per-expert totals and chunk prefixes, padded expert
 //           offsets, R and R_pad, per-expert tables           -> base[e][chunk]
-//   tokens  per token, routed entries                          -> tok[t]
-//   offsets one block: exclusive prefix of tok                 -> owner_offset
+//           exclusive prefix of tok                            -> owner_offset
 //   scatter per chunk: stable rank within the chunk, row, slot -> routed rows
-//   pad     per row < R_pad: expert of the row, padding rows, row-block tables
+//           per 256 rows < R_pad: expert of the row, padding rows, row-block tables
+#include <algorithm>
+
 #include "../../include/mk.h"
 #include "mk_internal.h"
 
@@ -48,17 +50,28 @@ __device__ __forceinline__ int local_expert(const IndexKParams& p, int64_t i) {
   return (e >= 0 && e < p.n_local) ? e : -1;
 }
 
+// Block b: the per-expert histogram of entry chunk b (b < nchunks) and the
+// routed-entry count of tokens 256b .. 256b+255 (the tokens pass, merged
+// into the same launch).
 __global__ __launch_bounds__(kChunk) void count_kernel(IndexKParams p) {
   extern __shared__ int h[];
-  for (int e = threadIdx.x; e < p.n_local; e += kChunk) h[e] = 0;
-  __syncthreads();
-  const int64_t i = (int64_t)blockIdx.x * kChunk + threadIdx.x;
-  if (i < (int64_t)p.T * p.topk) {
-    const int e = local_expert(p, i);
-    if (e >= 0) atomicAdd(&h[e], 1);
+  if ((int)blockIdx.x < p.nchunks) {
+    for (int e = threadIdx.x; e < p.n_local; e += kChunk) h[e] = 0;
+    __syncthreads();
+    const int64_t i = (int64_t)blockIdx.x * kChunk + threadIdx.x;
+    if (i < (int64_t)p.T * p.topk) {
+      const int e = local_expert(p, i);
+      if (e >= 0) atomicAdd(&h[e], 1);
+    }
+    __syncthreads();
+    for (int e = threadIdx.x; e < p.n_local; e += kChunk) p.hist[(int64_t)e * p.nchunks + blockIdx.x] = h[e];
   }
-  __syncthreads();
-  for (int e = threadIdx.x; e < p.n_local; e += kChunk) p.hist[(int64_t)e * p.nchunks + blockIdx.x] = h[e];
+  const int t = blockIdx.x * kChunk + threadIdx.x;
+  if (t < p.T) {
+    int c = 0;
+    for (int k = 0; k < p.topk; ++k) c += local_expert(p, (int64_t)t * p.topk + k) >= 0;
+    p.tok[t] = c;
+  }
 }
 
 // Block-wide exclusive scan of one value per thread (NT threads), total out.
@@ -138,67 +151,73 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(IndexKParams p) {
     const int off = p.exp_off[e];
     for (int c = lane; c < p.nchunks; c += 64) h[c] += off;
   }
-}
-
-__global__ __launch_bounds__(256) void tokens_kernel(IndexKParams p) {
-  const int t = blockIdx.x * 256 + threadIdx.x;
-  if (t >= p.T) return;
-  int c = 0;
-  for (int k = 0; k < p.topk; ++k) c += local_expert(p, (int64_t)t * p.topk + k) >= 0;
-  p.tok[t] = c;
-}
-
-__global__ __launch_bounds__(kPlanThreads) void offsets_kernel(IndexKParams p) {
-  __shared__ int s[kPlanThreads];
-  int carry = 0;
+  // token CSR offsets: exclusive prefix of the per-token counts (the
+  // offsets pass, merged into the same launch)
+  int tcarry = 0;
   for (int t0 = 0; t0 < p.T; t0 += kPlanThreads) {
     const int t = t0 + threadIdx.x;
     const int v = t < p.T ? p.tok[t] : 0;
     int tot;
     const int ex = block_exclusive_scan<kPlanThreads>(v, s, tot);
-    if (t < p.T && p.out.owner_offset) p.out.owner_offset[t] = carry + ex;
-    carry += tot;
+    if (t < p.T && p.out.owner_offset) p.out.owner_offset[t] = tcarry + ex;
+    tcarry += tot;
   }
-  if (threadIdx.x == 0 && p.out.owner_offset) p.out.owner_offset[p.T] = carry;
+  if (threadIdx.x == 0 && p.out.owner_offset) p.out.owner_offset[p.T] = tcarry;
 }
 
+// Block b: the routed rows of entry chunk b (b < nchunks), then rows
+// 256b .. 256b+255 of the padded table (the padding pass, merged into the
+// same launch; it writes every row's expert and the padding rows only, so
+// the two parts never write the same field).
 __global__ __launch_bounds__(kChunk) void scatter_kernel(IndexKParams p) {
-  __shared__ int ex[kChunk];
-  const int64_t i = (int64_t)blockIdx.x * kChunk + threadIdx.x;
-  const bool in = i < (int64_t)p.T * p.topk;
-  const int e = in ? local_expert(p, i) : -1;
-  ex[threadIdx.x] = e;
-  __syncthreads();
-  if (e < 0) return;
-  // stable rank among this chunk's earlier entries of the same expert
-  int rank = 0;
-  for (int j = 0; j < (int)threadIdx.x; ++j) rank += ex[j] == e;
-  const int64_t row = (int64_t)p.hist[(int64_t)e * p.nchunks + blockIdx.x] + rank;
-  const int t = (int)(i / p.topk), k = (int)(i % p.topk);
-  // slot: the token's routed entries in row order = (expert, k) order
-  int before = 0;
-  for (int k2 = 0; k2 < p.topk; ++k2) {
-    const int e2 = local_expert(p, (int64_t)t * p.topk + k2);
-    before += e2 >= 0 && (e2 < e || (e2 == e && k2 < k));
-  }
-  if (row >= p.cap) return;  // capacity exceeded: sizes reports R_pad > cap
+  constexpr int kWaves = kChunk / 64;
+  extern __shared__ int wcnt[];  // [kWaves][n_local]: per-wave counts of each expert
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const mk_moe_index& o = p.out;
-  if (o.pull_indices) {
-    o.pull_indices[3 * row + 0] = 0;
-    o.pull_indices[3 * row + 1] = 0;
-    o.pull_indices[3 * row + 2] = t;
+  if ((int)blockIdx.x < p.nchunks) {
+    const int64_t i = (int64_t)blockIdx.x * kChunk + threadIdx.x;
+    const int e = i < (int64_t)p.T * p.topk ? local_expert(p, i) : -1;
+    for (int x = lane; x < p.n_local; x += 64) wcnt[wave * p.n_local + x] = 0;
+    // stable rank among the chunk's earlier entries of the same expert:
+    // inside the wave by one ballot per distinct expert, plus the counts
+    // of the earlier waves
+    int rank = 0;
+    uint64_t pending = __ballot(e >= 0);
+    while (pending) {
+      const int el = __shfl(e, __builtin_ctzll(pending), 64);
+      const uint64_t m = __ballot(e == el);
+      if (e == el) rank = __popcll(m & ((1ull << lane) - 1ull));
+      if (lane == 0) wcnt[wave * p.n_local + el] = __popcll(m);
+      pending &= ~m;
+    }
+    __syncthreads();
+    if (e >= 0) {
+      for (int w = 0; w < wave; ++w) rank += wcnt[w * p.n_local + e];
+      const int64_t row = (int64_t)p.hist[(int64_t)e * p.nchunks + blockIdx.x] + rank;
+      const int t = (int)(i / p.topk), k = (int)(i % p.topk);
+      // slot: the token's routed entries in row order = (expert, k) order
+      int before = 0;
+      for (int k2 = 0; k2 < p.topk; ++k2) {
+        const int e2 = local_expert(p, (int64_t)t * p.topk + k2);
+        before += e2 >= 0 && (e2 < e || (e2 == e && k2 < k));
+      }
+      if (row < p.cap) {  // past the capacity: sizes reports R_pad > cap
+        if (o.pull_indices) {
+          o.pull_indices[3 * row + 0] = 0;
+          o.pull_indices[3 * row + 1] = 0;
+          o.pull_indices[3 * row + 2] = t;
+        }
+        if (o.row_weight) o.row_weight[row] = p.gates[i];
+        if (o.row_to_owner) o.row_to_owner[row] = 0;
+        if (o.owner_offset) {
+          const int slot = o.owner_offset[t] + before;
+          if (o.row_to_slot) o.row_to_slot[row] = slot;
+          if (o.slot_to_row) o.slot_to_row[slot] = (int32_t)row;
+        }
+      }
+    }
   }
-  if (o.row_weight) o.row_weight[row] = p.gates[i];
-  if (o.row_to_owner) o.row_to_owner[row] = 0;
-  if (o.owner_offset) {
-    const int slot = o.owner_offset[t] + before;
-    if (o.row_to_slot) o.row_to_slot[row] = slot;
-    if (o.slot_to_row) o.slot_to_row[slot] = (int32_t)row;
-  }
-}
-
-__global__ __launch_bounds__(256) void pad_kernel(IndexKParams p) {
-  const int64_t r = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t r = (int64_t)blockIdx.x * kChunk + threadIdx.x;
   const int64_t R_pad = p.sizes[1];
   if (r >= R_pad || r >= p.cap) return;
   // expert of row r: last e with exp_off[e] <= r (binary search)
@@ -209,11 +228,10 @@ __global__ __launch_bounds__(256) void pad_kernel(IndexKParams p) {
     else hi = mid - 1;
   }
   const int e = lo;
-  const int64_t i = r - p.exp_off[e];
+  const int64_t ie = r - p.exp_off[e];
   const int cnt = p.exp_cnt[e];
-  const mk_moe_index& o = p.out;
   if (o.row_expert) o.row_expert[r] = e;
-  if (i >= cnt) {
+  if (ie >= cnt) {
     if (o.pull_indices) {
       o.pull_indices[3 * r + 0] = -1;
       o.pull_indices[3 * r + 1] = -1;
@@ -226,7 +244,7 @@ __global__ __launch_bounds__(256) void pad_kernel(IndexKParams p) {
   if (r % p.row_block == 0) {
     const int64_t b = r / p.row_block;
     if (o.rb_expert) o.rb_expert[b] = e;
-    if (o.rb_rows) o.rb_rows[b] = (int)max((int64_t)0, min((int64_t)p.row_block, (int64_t)cnt - i));
+    if (o.rb_rows) o.rb_rows[b] = (int)max((int64_t)0, min((int64_t)p.row_block, (int64_t)cnt - ie));
   }
 }
 
@@ -254,13 +272,15 @@ hipError_t launch_build_indices(const int32_t* ids, const float* gates, int T, i
   p.sizes = sizes;
   p.out = out;
   // (no routed entries: plan sees nchunks = 0 and empty experts)
-  if (p.nchunks > 0)
-    hipLaunchKernelGGL(count_kernel, dim3(p.nchunks), dim3(kChunk), n_local * sizeof(int), stream, p);
+  const int64_t tblocks = ((int64_t)T + kChunk - 1) / kChunk;
+  const int64_t g1 = std::max<int64_t>(p.nchunks, tblocks);
+  if (g1 > 0)
+    hipLaunchKernelGGL(count_kernel, dim3((unsigned)g1), dim3(kChunk), n_local * sizeof(int), stream, p);
   hipLaunchKernelGGL(plan_kernel, dim3(1), dim3(kPlanThreads), 0, stream, p);
-  if (T > 0) hipLaunchKernelGGL(tokens_kernel, dim3((T + 255) / 256), dim3(256), 0, stream, p);
-  hipLaunchKernelGGL(offsets_kernel, dim3(1), dim3(kPlanThreads), 0, stream, p);
-  if (p.nchunks > 0) hipLaunchKernelGGL(scatter_kernel, dim3(p.nchunks), dim3(kChunk), 0, stream, p);
-  if (cap > 0) hipLaunchKernelGGL(pad_kernel, dim3((unsigned)((cap + 255) / 256)), dim3(256), 0, stream, p);
+  const int64_t g3 = std::max<int64_t>(p.nchunks, (cap + kChunk - 1) / kChunk);
+  if (g3 > 0)
+    hipLaunchKernelGGL(scatter_kernel, dim3((unsigned)g3), dim3(kChunk), (kChunk / 64) * n_local * sizeof(int), stream,
+                       p);
   return hipGetLastError();
 }
 
