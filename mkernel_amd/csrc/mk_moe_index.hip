@@ -74,21 +74,37 @@ __global__ __launch_bounds__(kChunk) void count_kernel(IndexKParams p) {
   }
 }
 
-// Block-wide exclusive scan of one value per thread (NT threads), total out.
+// Block-wide exclusive scan of one value per thread (NT threads), total out:
+// inclusive prefix sums inside each wave by shuffles, the wave totals
+// scanned by the first wave, two workgroup barriers in all.  `s` holds at
+// least NT / 64 + 1 ints.
 template <int NT>
 __device__ int block_exclusive_scan(int v, int* s, int& total) {
-  const int t = threadIdx.x;
-  s[t] = v;
-  __syncthreads();
-  for (int off = 1; off < NT; off <<= 1) {
-    const int x = t >= off ? s[t - off] : 0;
-    __syncthreads();
-    s[t] += x;
-    __syncthreads();
+  constexpr int W = NT / 64;
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  int incl = v;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int y = __shfl_up(incl, d, 64);
+    if (lane >= d) incl += y;
   }
-  total = s[NT - 1];
-  const int r = s[t] - v;
+  if (lane == 63) s[wave] = incl;
   __syncthreads();
+  if (wave == 0) {
+    const int wt = lane < W ? s[lane] : 0;
+    int wi = wt;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const int y = __shfl_up(wi, d, 64);
+      if (lane >= d) wi += y;
+    }
+    if (lane < W) s[lane] = wi - wt;       // exclusive prefix of the wave totals
+    if (lane == W - 1) s[W] = wi;          // block total
+  }
+  __syncthreads();
+  total = s[W];
+  const int r = s[wave] + incl - v;
+  __syncthreads();  // s is reused by the next scan
   return r;
 }
 
