@@ -292,12 +292,15 @@ def bench_moe(steps, warmup, extra):
     cap = (T_ * k_ + cfg.n_local * 127 + 127) // 128 * 128
     act_c = torch.empty((cap, cfg.I), dtype=torch.bfloat16, device="cuda")
     ye_c = torch.empty((cap, cfg.H), dtype=torch.bfloat16, device="cuda")
+    # K-split workspace made outside the capture (its one-time zero-fill must
+    # not be recorded into the graph)
+    ws_routed = ops.split_workspace()
 
     def routed_layer(i=0):
         tb = ops.moe_build_indices_dev(ids_d, gates_d, cfg.e0, cfg.n_local, sync=False)
         ops.moe_ffn_combine(tokens, tb["pull_indices"], tb["row_weight"], tb["owner_offset"], tb["slot_to_row"], w1,
                             w2, None, act_c, ye_c, y, rb_expert=tb["rb_expert"], rb_rows=tb["rb_rows"],
-                            fuse_dispatch=True, sizes=tb["sizes"])
+                            fuse_dispatch=True, sizes=tb["sizes"], split_ws=ws_routed)
 
     routed_layer()
     torch.cuda.synchronize()

@@ -41,7 +41,11 @@ def split_workspace(device=None, stream=None) -> torch.Tensor:
     (device, stream), mk_query_workspace_bytes() bytes, zero-filled once
     (every launch leaves it zeroed).  Launches on one stream are ordered, so
     they can share it; launches on different streams get different ones.
-    ``stream``: a torch stream, default the current stream of the device."""
+    ``stream``: a torch stream, default the current stream of the device.
+    Graph capture runs on a stream of its own: fetch the workspace before
+    capturing and pass it as ``split_ws``; one first created inside the
+    capture has its zero-fill recorded into the graph (about 11 us per
+    replay on MI355X)."""
     dev = torch.device("cuda", torch.cuda.current_device() if device is None else torch.device(device).index or 0)
     if stream is None:
         stream = torch.cuda.current_stream(dev)
