@@ -652,6 +652,11 @@ static int grouped_gemm_impl(const void* A, const void* W, void* out, const int3
   // fetch in one XCD's L2 (measured 15 us faster on config 5's GEMM1, and
   // 6 us slower on GEMM2's 14 column tiles, which keeps groups of 8).
   if (p.tiles_n <= 8) p.group_m = p.tiles_m;
+  // More column tiles without an epilogue (GEMM2: 7168 / 512 = 14): each
+  // expert's tiles together, column-major inside its run of row tiles
+  // (config-5 GEMM2 210.9 -> 203.7 us; GEMM1 + SwiGLU measured 6 us slower
+  // with it and keeps the order above).
+  if (p.tiles_n > 8 && mode == 0 && rb_expert) p.expert_order = 1;
   // The grouped GEMMs are bound by the chip's weight streaming.  When the
   // tail round cannot be K-split (more tail tiles than half the grid),
   // every workgroup runs the same number of whole-tile rounds either way;

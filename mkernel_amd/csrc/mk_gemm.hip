@@ -708,7 +708,25 @@ __device__ __forceinline__ void compute_role(const GemmKParams& p, int cons_id, 
   auto tile_body = [&](int t, bool permuted, int k0, int nk, f32x16 (&acc)[C::FM][C::FN], int& m0_out,
                        int& tn_out) __attribute__((always_inline)) {
     int tm, tn;
-    decode_grouped(t, tiles_m, p.tiles_n, p.group_m, tm, tn);
+    if (C::BM == 128 && p.expert_order) {
+      // Expert order: tile t lies in the run of row tiles [r0, r1) that
+      // share row tile t / tiles_n's expert (tiles t of that run are
+      // r0 * tiles_n .. r1 * tiles_n - 1, whatever the order inside it);
+      // inside the run, column-major.  A one-tile expert's column tiles
+      // are consecutive, so its activation rows are fetched once per XCD;
+      // a multi-tile expert's row tiles still stream each weight slice
+      // together.  The host sets this only with rb_expert.
+      const int rt = __builtin_amdgcn_readfirstlane(t / p.tiles_n);
+      const int e = __builtin_amdgcn_readfirstlane(p.rb_expert[rt]);
+      int r0 = rt, r1 = rt + 1;
+      while (r0 > 0 && __builtin_amdgcn_readfirstlane(p.rb_expert[r0 - 1]) == e) --r0;
+      while (r1 < tiles_m && __builtin_amdgcn_readfirstlane(p.rb_expert[r1]) == e) ++r1;
+      const int local = t - r0 * p.tiles_n, nr = r1 - r0;
+      tn = local / nr;
+      tm = r0 + local % nr;
+    } else {
+      decode_grouped(t, tiles_m, p.tiles_n, p.group_m, tm, tn);
+    }
     if (permuted) tm = row_perm[tm];
     // Tile coordinates are wave-uniform; keep them scalar.
     tm = __builtin_amdgcn_readfirstlane(tm);

@@ -23,6 +23,10 @@ struct GemmKParams {
   int M, N, K;
   int tiles_m, tiles_n;
   int group_m;
+  // 128-row grouped GEMMs with rb_expert: walk each expert's run of row
+  // tiles column by column (one expert's tiles consecutive) instead of the
+  // grouped order
+  int expert_order;
   // grid roles
   int n_prod, n_cons;
   int xcd_remap;

@@ -54,6 +54,36 @@ def test_grouped_gemm1(dev, use_rb, skip_pad, split, tile_n):
     assert (out.cpu()[torch.from_numpy(pad)] == 0).all()  # zero rows stay zero
 
 
+MANY = wl.MoeCfg(tokens=1024, H=256, I=2304, experts=64, topk=8, ep=8, rank=0)
+
+
+@pytest.mark.parametrize("split", [None, False])
+def test_grouped_gemm_many_column_tiles(dev, split):
+    """More than 8 column tiles and no epilogue (GEMM2's shape class: 9 or
+    18 column tiles here), where the tiles walk each expert's run of row
+    tiles together, including a multi-tile expert: every row matches the
+    oracle, padding rows stay zero, and without a K-split both tile widths
+    give the same bits."""
+    _say(f"moe grouped gemm, many column tiles, split={split}")
+    tokens, ids, gates, w1, w2, idx, d = _setup(dev, MANY)
+    assert (idx["padded_tokens_per_expert"] > 128).any()  # some expert spans several row tiles
+    post = om.permute_ref(tokens, idx["pull_indices"])
+    outs = []
+    for tile_n in (512, 256):
+        out = torch.full((idx["R_pad"], 2 * MANY.I), 3.0, dtype=torch.bfloat16, device=dev)
+        ops.moe_grouped_gemm(post.to(dev), w1.to(dev), out, rb_expert=d["rb_expert"], mode=0,
+                             rb_rows=d["rb_rows"], split_ws=split, tile_n=tile_n)
+        torch.cuda.synchronize()
+        outs.append(out.cpu())
+    ref = om.grouped_gemm_ref(post, w1, idx["padded_tokens_per_expert"])
+    pad = torch.from_numpy(idx["pull_indices"][:, 0] < 0)
+    for out in outs:
+        assert rel_fro(out.float(), ref) < TOL
+        assert (out[pad] == 0).all()
+    if split is False:
+        assert torch.equal(outs[0], outs[1])
+
+
 @pytest.mark.parametrize("tile_n", [256, 512])
 @pytest.mark.parametrize("split", [None, False])
 def test_gemm1_swiglu(dev, split, tile_n):
