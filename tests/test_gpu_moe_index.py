@@ -99,6 +99,8 @@ def test_index_dev_feeds_ffn(dev):
 # --- the routed layer with the row count left on the device -----------------
 
 LAYER = wl.MoeCfg(tokens=512, H=512, I=256, experts=64, topk=8, ep=8, rank=0)
+# GEMM2 with 9 column tiles of 512 (more than 8: the expert tile order)
+LAYER_WIDE = wl.MoeCfg(tokens=512, H=4608, I=256, experts=64, topk=8, ep=8, rank=0)
 
 
 def _host_layer(dev, cfg, tokens, w1, w2, ids, gates, split_ws, fuse):
@@ -145,14 +147,17 @@ def _routing(cfg, seed):
     return np.ascontiguousarray(ids, np.int32), np.ascontiguousarray(gates, np.float32)
 
 
+@pytest.mark.parametrize("wide", [False, True])
 @pytest.mark.parametrize("fuse", [False, True])
-def test_layer_with_device_row_count(dev, fuse):
+def test_layer_with_device_row_count(dev, fuse, wide):
     """Without the K-split every output tile is one workgroup's full-K sum,
     so the capacity-sized launch gives the host-sized launch's bits; with the
-    split (planned on the device) it stays within the parity bound."""
-    _say(f"moe layer, device row count, fuse={fuse}")
+    split (planned on the device) it stays within the parity bound.  wide:
+    GEMM2 has more than 8 column tiles, so both launches walk the tiles in
+    expert order, the device one over its clamped row tiles."""
+    _say(f"moe layer, device row count, fuse={fuse} wide={wide}")
     from oracle.gemm import rel_fro
-    cfg = LAYER
+    cfg = LAYER_WIDE if wide else LAYER
     tokens, _, _, w1, w2 = wl.moe_inputs(cfg)
     tokens, w1, w2 = tokens.to(dev), w1.to(dev), w2.to(dev)
     ids, gates = _routing(cfg, 6)
