@@ -115,6 +115,8 @@ def bench_ag(steps, warmup, producers, extra):
         # cooperative staging with every workgroup copying before every round
         "even_share": lambda i: gated(i, -2),
         "dedicated": lambda i: gated(i, 32),
+        # one-wave staging workgroups co-resident with a register-capped GEMM
+        "coresident": lambda i: gated(i, -3),
         "ungated": lambda i: ops.ag_gemm(None, A_full, B, C, None, None, epoch=1, gated=False, num_producers=0),
         # gated, flags already published (pure gating cost, all CUs computing)
         "preset": lambda i: ops.ag_gemm(None, A_full, B, C, flags_pub, order_d, epoch=2 ** 30, num_producers=0),
@@ -131,6 +133,7 @@ def bench_ag(steps, warmup, producers, extra):
         "us_ungated": ms_ungated * 1e3, "us_gated_flags_preset": ms_preset * 1e3,
         "us_gated_32_dedicated_producers": ms_dedicated * 1e3,
         "us_gated_even_share_staging": r["even_share"] * 1e3,
+        "us_gated_coresident_staging_kernel": r["coresident"] * 1e3,
         "tflops_gated_producer": flops / ms / 1e9, "tflops_ungated": flops / ms_ungated / 1e9,
         "gating_overhead_producer": ms_med / ms_ungated - 1.0,
         "gating_overhead_flag_check": ms_preset / ms_ungated - 1.0,

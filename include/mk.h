@@ -80,7 +80,19 @@ int mk_gemm(const mk_gemm_args* args, void* stream);
  *                            4-7) take turns: one copies ahead for the next
  *                            round while the other computes
  *   gated, producers == -2 : cooperative staging with every workgroup
- *                            copying an even share before every round    */
+ *                            copying an even share before every round
+ *   gated, producers <= -3 : wave-specialised producer: a staging kernel of
+ *                            (-2 - producers) one-wave workgroups per
+ *                            compute workgroup (1..4) runs beside a GEMM
+ *                            capped at 224 VGPRs (room for one 64-VGPR
+ *                            staging wave per SIMD) on a library side
+ *                            stream, forked from and joined back into
+ *                            `stream`; pieces are claimed in stage order
+ *                            from a word in split_ws (required), the
+ *                            compute workgroups claiming what a round
+ *                            still lacks.  Under graph capture the call
+ *                            stages cooperatively (-1) instead.  Needs
+ *                            stage_counters. */
 typedef struct mk_ag_gemm_args {
   const void* A_shards;  /* bf16 [M, K]: shards stacked in rank order (source) */
   void* A_full;          /* bf16 [M, K]: gathered A (destination / GEMM input) */

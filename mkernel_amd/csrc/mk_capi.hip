@@ -107,6 +107,9 @@ int check_gemm_shape(int64_t M, int64_t N, int64_t K, int bm, int64_t lda = 0, i
 
 constexpr int64_t kSplitTileBytes = 256 * 256 * 4;  // one fp32 partial tile (BM x BN <= 256 x 256)
 constexpr int64_t kSplitFlagBytes = 4096;           // flag words at the start of the workspace
+// The last 64 bytes of the flag area hold the claim word of co-resident
+// staging (epoch-stamped, never reset); K-split flags use the bytes before.
+constexpr int64_t kClaimOffset = kSplitFlagBytes - 64;
 
 int64_t split_ws_bytes(int cus) { return kSplitFlagBytes + (int64_t)cus * kSplitTileBytes; }
 
@@ -124,7 +127,7 @@ void plan_split(mk::GemmKParams& p, int bm, void* ws, int64_t ws_bytes, int bn =
   s = std::min(s, (p.K / 32) / 4);  // keep every part at >= 4 K stages
   if (s < 2) return;
   const int64_t parts = (int64_t)R * (s - 1);
-  if (parts * 4 > kSplitFlagBytes || kSplitFlagBytes + parts * bm * bn * 4 > ws_bytes) return;
+  if (parts * 4 > kClaimOffset || kSplitFlagBytes + parts * bm * bn * 4 > ws_bytes) return;
   p.sk_flags = static_cast<uint32_t*>(ws);
   p.sk_ws = reinterpret_cast<float*>(static_cast<char*>(ws) + kSplitFlagBytes);
   p.sk_full = ntiles - R;
@@ -283,10 +286,23 @@ int mk_ag_gemm(const mk_ag_gemm_args* a, void* stream) {
     if (nflags + a->M / bm > 8192)
       return fail(MK_ESHAPE, "mk_ag_gemm: too many flags for the schedule scratch");
   }
-  if (a->num_producers < -2) return fail(MK_EINVAL, "mk_ag_gemm: num_producers must be >= -2");
+  if (a->num_producers < -6) return fail(MK_EINVAL, "mk_ag_gemm: num_producers must be >= -6");
   if (a->gated && a->num_producers != 0 && !a->A_shards)
     return fail(MK_EINVAL, "mk_ag_gemm: staging needs A_shards");
   const bool coop = a->gated && a->num_producers < 0;
+  // num_producers <= -3: co-resident staging kernel, -2 - num_producers
+  // one-wave workgroups per CU beside the GEMM
+  int costage_waves = (a->gated && a->num_producers <= -3) ? -2 - a->num_producers : 0;
+  if (costage_waves) {
+    // Under graph capture the fork/join would become two graph branches
+    // whose order the replay does not fix; stage cooperatively instead.
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    hipError_t ce = hipStreamIsCapturing(static_cast<hipStream_t>(stream), &cap);
+    if (ce != hipSuccess) return hip_fail(ce, "mk_ag_gemm hipStreamIsCapturing");
+    if (cap != hipStreamCaptureStatusNone) costage_waves = 0;
+  }
+  if (costage_waves && (!a->split_ws || a->split_ws_bytes < kSplitFlagBytes))
+    return fail(MK_EINVAL, "mk_ag_gemm: co-resident staging keeps its claim word in split_ws, which is NULL or short");
   if (coop && !a->stage_counters) return fail(MK_EINVAL, "mk_ag_gemm: cooperative staging needs stage_counters");
   int total;
   if (int rc = grid_total(a->num_cus, d, "mk_ag_gemm", &total)) return rc;
@@ -323,13 +339,18 @@ int mk_ag_gemm(const mk_ag_gemm_args* a, void* stream) {
       p.st_present = a->n_present;
       p.st_flags = a->flags;
       p.st_counters = a->stage_counters;
-      p.st_coop = coop ? (a->num_producers == -1 ? 2 : 1) : 0;  // -1: halves alternate windows
+      // -1: halves alternate windows; -2: even share; <= -3: claimed
+      p.st_coop = costage_waves ? 3 : coop ? (a->num_producers == -2 ? 1 : 2) : 0;
       p.st_batch = 8;
+      if (costage_waves)
+        p.st_claim = reinterpret_cast<uint32_t*>(static_cast<char*>(a->split_ws) + kClaimOffset);
     }
   }
   if (int rc = check_ws(a->split_ws, a->split_ws_bytes, "mk_ag_gemm")) return rc;
   plan_split(p, bm, a->split_ws, a->split_ws_bytes);
-  hipError_t e = mk::launch_gemm(p, bm, mk::kEpiStore, static_cast<hipStream_t>(stream));
+  hipError_t e = costage_waves ? mk::launch_gemm_costaged(p, mk::kEpiStore, costage_waves * total,
+                                                          static_cast<hipStream_t>(stream))
+                               : mk::launch_gemm(p, bm, mk::kEpiStore, static_cast<hipStream_t>(stream));
   return e == hipSuccess ? MK_OK : hip_fail(e, "mk_ag_gemm launch");
 }
 
@@ -678,7 +699,7 @@ static int grouped_gemm_impl(const void* A, const void* W, void* out, const int3
     // consumer (and one flag word each).
     p.rows_dev = sizes + 1;
     p.spread_dev = num_cus <= 0 ? 1 : 0;  // the library's grid: the kernel applies the tail spread
-    if (split_ws && p.waves == 8 && (int64_t)p.n_cons * 4 <= kSplitFlagBytes &&
+    if (split_ws && p.waves == 8 && (int64_t)p.n_cons * 4 <= kClaimOffset &&
         split_ws_bytes >= kSplitFlagBytes + (int64_t)p.n_cons * 128 * bn * 4) {
       p.sk_dev = 1;
       p.sk_flags = static_cast<uint32_t*>(split_ws);

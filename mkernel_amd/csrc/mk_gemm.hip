@@ -32,6 +32,8 @@
 #include "mk_device.h"
 #include "mk_internal.h"
 #include "mk_once.h"
+#include <mutex>
+#include <vector>
 
 namespace mk {
 
@@ -144,52 +146,128 @@ __device__ void producer_role(const GemmKParams& p, int pid) {
   }
 }
 
-// Cooperative staging: every compute workgroup copies its share of the
-// staging pieces (kPieces per 128-row block; global piece q is piece
-// q % kPieces of the block at stage position q / kPieces; a workgroup
-// copies pieces q, q + stride, ... — stride n_cons when every workgroup
-// shares a range, the group size when one half of the grid does).  Each finished piece bumps its block's
-// counter; the workgroup whose increment completes the block publishes the
-// block's flag.  Counters are never reset: completion is detected modulo
-// kPieces.  A workgroup stages in increasing q and may stop at any limit and
-// resume later (q and batch are its cursor), which lets the copy run between
-// tile rounds instead of all before the first one.
-template <int NT>
-__device__ void coop_stage(const GemmKParams& p, int stride, int& q, int& batch, int limit) {
+// One staging piece: global piece q is piece q % kPieces of the 128-row
+// block at stage position q / kPieces.  Copied by the NT threads that call
+// this (U loads in flight per thread); blocks at the first st_present
+// positions are already in place (this rank's own shard) and are counted and
+// published without a copy.  Returns the piece's block.
+template <int NT, int U>
+__device__ __forceinline__ int stage_piece(const GemmKParams& p, int q) {
   const int64_t block_elems = (int64_t)kFlagRows * p.st_cols;
   const int64_t piece_vec = block_elems / 8 / kPieces;  // 16-byte units per piece
+  const int pos = q / kPieces, piece = q % kPieces;
+  const int b = p.st_order ? p.st_order[pos] : pos;
+  const int64_t off = (int64_t)b * block_elems + (int64_t)piece * piece_vec * 8;
+  if (pos >= p.st_present) copy_wt<NT, U>(p.st_src + off, p.st_dst + off, piece_vec);
+  return b;
+}
+
+// One finished piece of block b (its stores performed at agent scope by
+// every thread that made them): bump the block's counter; the increment
+// that completes the block publishes the block's flag.  The increments form
+// one chain per block, so a relaxed agent-scope flag store suffices.
+// Counters are never reset: completion is detected modulo kPieces.
+__device__ __forceinline__ void count_piece(const GemmKParams& p, int b) {
+  const uint32_t old = __hip_atomic_fetch_add(p.st_counters + b, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (old % kPieces == kPieces - 1)
+    __hip_atomic_store(p.st_flags + b, launch_epoch(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Cooperative staging: every compute workgroup copies its share of the
+// staging pieces (a workgroup copies pieces q, q + stride, ... — stride
+// n_cons when every workgroup shares a range, the group size when one half
+// of the grid does).  A workgroup stages in increasing q and may stop at any
+// limit and resume later (q and batch are its cursor), which lets the copy
+// run between tile rounds instead of all before the first one.
+template <int NT>
+__device__ void coop_stage(const GemmKParams& p, int stride, int& q, int& batch, int limit) {
   limit = min(limit, p.st_nblocks * kPieces);
-  auto copy_piece = [&](int qq) {
-    const int pos = qq / kPieces, piece = qq % kPieces;
-    const int b = p.st_order ? p.st_order[pos] : pos;
-    const int64_t off = (int64_t)b * block_elems + (int64_t)piece * piece_vec * 8;
-    // blocks at the first st_present positions are already in place (this
-    // rank's own shard): counted and published, not copied
-    if (pos >= p.st_present) copy_wt<NT, 16>(p.st_src + off, p.st_dst + off, piece_vec);
-    return b;
-  };
-  // The counter increments form one chain per block; each is made after
-  // its workgroup's pieces were performed at agent scope (copy_wt), so the
-  // workgroup whose increment completes the block may publish the flag with
-  // a relaxed agent-scope store.
-  auto count_piece = [&](int b) {
-    const uint32_t old = __hip_atomic_fetch_add(p.st_counters + b, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (old % kPieces == kPieces - 1)
-      __hip_atomic_store(p.st_flags + b, launch_epoch(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  };
   // Pieces are counted in batches of p.st_batch: copy the batch, wait for
   // the stores, one barrier, then count the batch's pieces; the first batch
   // is a single piece so the earliest blocks complete early.
   while (q < limit) {
     int bs[8];
     int n = 0;
-    for (; n < batch && q < limit; ++n, q += stride) bs[n] = copy_piece(q);
+    for (; n < batch && q < limit; ++n, q += stride) bs[n] = stage_piece<NT, 16>(p, q);
     wait_vmem_all();
     __syncthreads();
     if (threadIdx.x == 0)
-      for (int i = 0; i < n; ++i) count_piece(bs[i]);
+      for (int i = 0; i < n; ++i) count_piece(p, bs[i]);
     batch = p.st_batch;
   }
+}
+
+// Claimed staging (st_coop 3), the compute workgroups' side: pieces are
+// handed out in stage order through the launch's claim word (st_claim[0]),
+// which the co-resident staging kernel (stage_kernel) draws from one piece
+// at a time.  Before a tile round, a workgroup that finds pieces below
+// `need` (what the round waits for) still unclaimed claims its 1/n_cons
+// share of them and copies it; when the staging kernel is ahead, it copies
+// nothing.  The claim word starts every launch at zero: each claimer
+// (staging wave or compute workgroup) bumps st_claim[1] once it will claim
+// no more, and the last of them zeroes both words for the next launch.
+template <int NT>
+__device__ void claim_stage(const GemmKParams& p, int need, int n_cons, int* sh) {
+  const int total = p.st_nblocks * kPieces;
+  need = min(need, total);
+  if (threadIdx.x == 0) {
+    const int done = (int)__hip_atomic_load(p.st_claim, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    int first = 0, n = 0;
+    if (done < need) {
+      const int share = (need - done + n_cons - 1) / n_cons;
+      first = (int)__hip_atomic_fetch_add(p.st_claim, (uint32_t)share, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      n = max(0, min(share, total - first));
+    }
+    sh[0] = first;
+    sh[1] = n;
+  }
+  __syncthreads();
+  const int first = sh[0], n = sh[1];
+  __syncthreads();  // sh is free again
+  for (int i0 = 0; i0 < n; i0 += 8) {
+    int bs[8];
+    const int m = min(8, n - i0);
+    for (int i = 0; i < m; ++i) bs[i] = stage_piece<NT, 16>(p, first + i0 + i);
+    wait_vmem_all();
+    __syncthreads();
+    if (threadIdx.x == 0)
+      for (int i = 0; i < m; ++i) count_piece(p, bs[i]);
+  }
+}
+
+// A claimer that will claim no more pieces in this launch checks out; the
+// last of the `participants` zeroes the claim word and the check-out count.
+__device__ __forceinline__ void claim_checkout(const GemmKParams& p, uint32_t participants) {
+  if (__hip_atomic_fetch_add(p.st_claim + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == participants - 1) {
+    __hip_atomic_store(p.st_claim, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(p.st_claim + 1, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
+// The co-resident staging kernel: one-wave workgroups that copy pieces in
+// stage order, drawing one piece at a time from the claim word (the next
+// claim is issued before the current piece's copy, so its latency hides
+// behind the copy), and count/publish each piece like the compute
+// workgroups do.  64 VGPRs and no LDS: the register-capped GEMM leaves that
+// room on every SIMD, so these waves run beside the GEMM's workgroups — the
+// copy overlaps the MFMA work instead of taking turns with it (reference:
+// the intra_comm_sm copy of src/ag_gemm.cu:49-83 running beside
+// fused_comp_sm, :265-461).
+__global__ __launch_bounds__(64) __attribute__((amdgpu_num_vgpr(32))) void stage_kernel(GemmKParams p) {
+  const int total = p.st_nblocks * kPieces;
+  int c = 0;
+  if (threadIdx.x == 0) c = (int)__hip_atomic_fetch_add(p.st_claim, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  c = __builtin_amdgcn_readfirstlane(c);
+  while (c < total) {
+    int next = 0;
+    if (threadIdx.x == 0)
+      next = (int)__hip_atomic_fetch_add(p.st_claim, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const int b = stage_piece<64, 8>(p, c);
+    wait_vmem_all();  // this wave's stores are performed at agent scope
+    if (threadIdx.x == 0) count_piece(p, b);
+    c = __builtin_amdgcn_readfirstlane(next);
+  }
+  if (threadIdx.x == 0) claim_checkout(p, gridDim.x + p.st_claimers);
 }
 
 // ---------------------------------------------------------------------------
@@ -481,6 +559,7 @@ struct StagePlan {
   int n_rounds;
   int q, batch;           // coop_stage cursor (even-share mode)
   int grp, gid, gsize;    // alternating mode: half of the grid (0/1), id in it, its size (0: even share)
+  bool claim;             // claimed mode: before round w, claim a share of what round w needs and is unclaimed
 };
 
 // Piece count that rounds 0..r need staged (r = n_rounds: every piece).
@@ -763,9 +842,10 @@ __device__ __forceinline__ void compute_role(const GemmKParams& p, int cons_id, 
 
     // Flag gate on the A rows of this tile (AllGather consumer side).
     if (p.a_flags) {
-      if (tid == 0)
-        wait_flags<C::BM / kFlagRows>([&](int f) { return p.a_flags + m0 / kFlagRows + f; }, C::BM / kFlagRows, launch_epoch(p), p.spin_limit,
-                   p.err);
+      if (tid == 0) {
+        wait_flags<C::BM / kFlagRows>([&](int f) { return p.a_flags + m0 / kFlagRows + f; }, C::BM / kFlagRows,
+                                      launch_epoch(p), p.spin_limit, p.err);
+      }
       __syncthreads();
     }
 
@@ -1033,7 +1113,9 @@ __device__ __forceinline__ void compute_role(const GemmKParams& p, int cons_id, 
   // the arrival order.
   const int st_total = p.st_nblocks * kPieces;
   for (int w = 0; w < n_full_mine; ++w) {
-    if (sp.round_need && sp.gsize > 0 && w < sp.n_rounds) {
+    if (sp.claim) {
+      claim_stage<C::NT>(p, need_pieces(p, sp, w), n_cons, reinterpret_cast<int*>(smem));
+    } else if (sp.round_need && sp.gsize > 0 && w < sp.n_rounds) {
       alt_stage<C::NT>(p, cons_id, sp, w);
     } else if (sp.round_need) {
       // this tile is in round w: stage what round w waits for, and at least
@@ -1049,7 +1131,15 @@ __device__ __forceinline__ void compute_role(const GemmKParams& p, int cons_id, 
     tile_body(t, row_perm != nullptr, 0, nk_all, acc, m0, tn);
     store_tile<C, EPI>(p, acc, m0, tn, tid, smem);
   }
-  if (sp.round_need && sp.gsize == 0) coop_stage<C::NT>(p, n_cons, sp.q, sp.batch, st_total);
+  if (sp.round_need && !sp.claim && sp.gsize == 0) coop_stage<C::NT>(p, n_cons, sp.q, sp.batch, st_total);
+  // claimed mode: the K-split tail tiles may wait for pieces past every
+  // whole round's need; claim whatever is still unclaimed (normally nothing:
+  // the staging kernel is ahead), so no piece is left to a kernel that might
+  // not be running
+  if (sp.claim) {
+    claim_stage<C::NT>(p, st_total, n_cons, reinterpret_cast<int*>(smem));
+    if (tid == 0) claim_checkout(p, p.st_claimers + p.st_stage_waves);
+  }
   // alternating mode: a consumer with no tile in the last whole round
   // still copies its shares of the ranges staged before that round
   if (sp.round_need && sp.gsize > 0)
@@ -1233,7 +1323,7 @@ __device__ void build_full_list(const GemmKParams& p, const int* row_perm, uint1
 }
 
 template <int BM, int WAVES, int EPI, int BN>
-__global__ __launch_bounds__(64 * WAVES, 1) void gemm_kernel(GemmKParams p) {
+__device__ __forceinline__ void gemm_main(const GemmKParams& p) {
   using C = Cfg<BM, WAVES, BN>;
   extern __shared__ __attribute__((aligned(16))) char smem[];
   if ((int)blockIdx.x < p.n_prod) {
@@ -1273,6 +1363,7 @@ __global__ __launch_bounds__(64 * WAVES, 1) void gemm_kernel(GemmKParams p) {
   sp.n_rounds = 0;
   sp.round_need = nullptr;
   sp.grp = sp.gid = sp.gsize = 0;
+  sp.claim = false;
   if constexpr (C::kSched) {
     __shared__ int row_perm[kMaxTilesM];
     __shared__ uint16_t full_list[kMaxSplitListTiles];
@@ -1299,11 +1390,16 @@ __global__ __launch_bounds__(64 * WAVES, 1) void gemm_kernel(GemmKParams p) {
         build_round_need<C::NT>(p, full, n_rounds, flist, row_key, round_need);
         sp.n_rounds = n_rounds;
         sp.round_need = round_need;
+        sp.claim = p.st_coop == 3;
         if (p.st_coop == 2 && p.xcd_remap && n_rounds >= 1) {
           sp.gsize = p.n_cons / 2;
           sp.grp = cons / sp.gsize;
           sp.gid = cons % sp.gsize;
         }
+      } else if (p.st_coop == 3) {
+        // no per-round needs known: claim an even share of everything now
+        claim_stage<C::NT>(p, p.st_nblocks * kPieces, p.n_cons, reinterpret_cast<int*>(smem));
+        if (threadIdx.x == 0) claim_checkout(p, p.st_claimers + p.st_stage_waves);
       } else {
         coop_stage<C::NT>(p, p.n_cons, sp.q, sp.batch, p.st_nblocks * kPieces);
       }
@@ -1316,6 +1412,22 @@ __global__ __launch_bounds__(64 * WAVES, 1) void gemm_kernel(GemmKParams p) {
     if (p.st_coop) coop_stage<C::NT>(p, p.n_cons, sp.q, sp.batch, p.st_nblocks * kPieces);
     compute_role<C, EPI>(p, cons, n_cons, smem, nullptr, nullptr, sp);
   }
+}
+
+template <int BM, int WAVES, int EPI, int BN>
+__global__ __launch_bounds__(64 * WAVES, 1) void gemm_kernel(GemmKParams p) {
+  gemm_main<BM, WAVES, EPI, BN>(p);
+}
+
+// The 256 x 256 GEMM that runs beside the staging kernel, capped at 224
+// VGPRs per wave (the attribute counts in units of two registers on gfx950,
+// whose waves draw VGPRs and AGPRs from one 512-entry file per SIMD lane):
+// its two waves per SIMD leave 64 registers on every SIMD for one staging
+// wave.  The K loop stays spill-free at this cap (the extra spills are in
+// the tile set-up and the K-split exchange).
+template <int EPI>
+__global__ __launch_bounds__(512, 1) __attribute__((amdgpu_num_vgpr(112))) void gemm_kernel_capped(GemmKParams p) {
+  gemm_main<256, 8, EPI, 256>(p);
 }
 
 // One thread: *epoch_ptr + 1, skipping 0 (a vector store, ordered before
@@ -1360,6 +1472,71 @@ static hipError_t launch_t(const GemmKParams& p, hipStream_t stream) {
 template <int BM, int EPI>
 static hipError_t launch_w(const GemmKParams& p, hipStream_t stream) {
   return p.waves == 8 ? launch_t<BM, 8, EPI, 256>(p, stream) : launch_t<BM, 4, EPI, 256>(p, stream);
+}
+
+// Side stream and fork/join events of the co-resident staging, one set per
+// device, created on first use and kept until the process ends.
+struct CostageStreams {
+  hipStream_t side = nullptr;
+  hipEvent_t fork = nullptr, join = nullptr;
+};
+
+static hipError_t costage_streams(int dev, CostageStreams** out) {
+  static std::mutex mu;
+  static std::vector<CostageStreams> per_dev;
+  std::lock_guard<std::mutex> lock(mu);
+  if ((int)per_dev.size() <= dev) per_dev.resize(dev + 1);
+  CostageStreams& c = per_dev[dev];
+  if (!c.side) {
+    hipError_t e = hipStreamCreateWithFlags(&c.side, hipStreamNonBlocking);
+    if (e == hipSuccess) e = hipEventCreateWithFlags(&c.fork, hipEventDisableTiming);
+    if (e == hipSuccess) e = hipEventCreateWithFlags(&c.join, hipEventDisableTiming);
+    if (e != hipSuccess) return e;
+  }
+  *out = &c;
+  return hipSuccess;
+}
+
+hipError_t launch_gemm_costaged(const GemmKParams& p, int epi, int n_stage_waves, hipStream_t stream) {
+  using C = Cfg<256, 8, 256>;
+  if (p.waves != 8 || p.st_coop != 3 || !p.st_claim || n_stage_waves < 1) return hipErrorInvalidValue;
+  if (epi != kEpiStore && epi != kEpiReduce) return hipErrorInvalidValue;
+  const void* fn = epi == kEpiReduce ? reinterpret_cast<const void*>(&gemm_kernel_capped<kEpiReduce>)
+                                     : reinterpret_cast<const void*>(&gemm_kernel_capped<kEpiStore>);
+  static PerDeviceFlag attr_set[2];
+  PerDeviceFlag& flag = attr_set[epi == kEpiReduce ? 1 : 0];
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (!flag.is_set(dev)) {
+    e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, C::LDS_BYTES);
+    if (e != hipSuccess) return e;
+    flag.set(dev);
+  }
+  CostageStreams* cs = nullptr;
+  if ((e = costage_streams(dev, &cs)) != hipSuccess) return e;
+  // Fork: the staging kernel is enqueued first, on the side stream, after
+  // everything already on `stream`; the GEMM follows on `stream`; the join
+  // makes later work on `stream` wait for both.  The two kernels run
+  // concurrently when the streams sit on different hardware queues (the
+  // GEMM's register cap leaves room for the staging waves on every SIMD);
+  // on one queue they run one after the other, staging first.  Either way
+  // nothing waits in a cycle: the staging waves wait on nothing.
+  GemmKParams pg = p;
+  // claimers that check out of the claim word: every compute workgroup and
+  // every staging wave
+  pg.st_claimers = p.n_cons;
+  pg.st_stage_waves = n_stage_waves;
+  if ((e = hipEventRecord(cs->fork, stream)) != hipSuccess) return e;
+  if ((e = hipStreamWaitEvent(cs->side, cs->fork, 0)) != hipSuccess) return e;
+  hipLaunchKernelGGL(stage_kernel, dim3(n_stage_waves), dim3(64), 0, cs->side, pg);
+  if ((e = hipGetLastError()) != hipSuccess) return e;
+  if ((e = hipEventRecord(cs->join, cs->side)) != hipSuccess) return e;
+  GemmKParams pk = pg;
+  void* args[] = {&pk};
+  if ((e = hipLaunchKernel(fn, dim3(p.n_prod + p.n_cons), dim3(C::NT), args, C::LDS_BYTES, stream)) != hipSuccess)
+    return e;
+  return hipStreamWaitEvent(stream, cs->join, 0);
 }
 
 // Tile BM x bn; bn = 512 exists for BM = 128 with the store and SwiGLU

@@ -61,7 +61,12 @@ struct GemmKParams {
   const int* st_order;
   uint32_t* st_flags;
   uint32_t* st_counters;    // cooperative staging: pieces completed per block (mod kPieces)
-  int st_coop;              // 1: every workgroup stages its pieces before computing
+  int st_coop;              // 1: even share, 2: alternating halves, 3: claimed (co-resident staging kernel)
+  // st_coop 3: [0] the next unclaimed piece, shared with the staging kernel;
+  // [1] claimers checked out; the last of st_claimers compute workgroups +
+  // st_stage_waves staging waves to check out zeroes both
+  uint32_t* st_claim;
+  int st_claimers, st_stage_waves;
   int st_batch;             // pieces per release after the first (1..8)
   // K-split of the tail round: tiles >= sk_full are split sk_split ways along
   // K (sk_split <= 1: no split); partials go through sk_ws with sk_flags
@@ -85,6 +90,10 @@ struct GemmKParams {
 };
 
 hipError_t launch_gemm(const GemmKParams& p, int bm, int epi, hipStream_t stream, int bn = 256);
+// Co-resident staging: the one-wave staging kernel (waves_per_cu per CU)
+// followed by a register-capped 256 x 256 GEMM that may start while the
+// staging kernel runs; both claim pieces through p.st_claim.
+hipError_t launch_gemm_costaged(const GemmKParams& p, int epi, int n_stage_waves, hipStream_t stream);
 hipError_t launch_epoch_advance(uint32_t* epoch_ptr, hipStream_t stream);
 
 struct PermuteKParams {

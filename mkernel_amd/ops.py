@@ -93,8 +93,10 @@ def ag_gemm(A_shards, A_full, B, C_out, flags, stage_order, epoch: int, gated: b
     (advanced by epoch_advance, e.g. inside a recorded graph).  num_producers
     -1 (default) stages cooperatively, the two halves of the grid taking
     turns to copy ahead; -2 stages cooperatively with every workgroup copying
-    an even share before every round.  Both need stage_counters (int32
-    [M/128], zeroed once).  n_present: the first n_present blocks of
+    an even share before every round; -3 .. -6 run a staging kernel of
+    (-2 - num_producers) one-wave workgroups per CU beside the GEMM on a
+    side stream (the wave-specialised producer role).  All of them need
+    stage_counters (int32 [M/128], zeroed once).  n_present: the first n_present blocks of
     stage_order are already in A_full (published, not copied)."""
     _bf16(A_full, "A_full"); _bf16(B, "B"); _bf16(C_out, "C")
     M, K = A_full.shape

@@ -110,7 +110,7 @@ def _ag_case(dev, world=8, shard=256, K=512, N=512, seed=0):
     return cfg, A, B, torch.from_numpy(order)
 
 
-@pytest.mark.parametrize("producers", [-1, -2, 1, 4, 16])
+@pytest.mark.parametrize("producers", [-1, -2, 1, 4, 16, -3, -4, -6])
 def test_ag_gemm_producer_gated(dev, producers):
     _say(f"ag_gemm producers={producers}")
     cfg, A, B, order = _ag_case(dev)
@@ -130,6 +130,11 @@ def test_ag_gemm_producer_gated(dev, producers):
     ops.ag_gemm(None, A_full, Bd, C2, None, None, epoch=1, gated=False, num_producers=0)
     torch.cuda.synchronize()
     assert torch.equal(C.cpu(), C2.cpu())
+    if producers <= -3:
+        # the co-resident staging leaves its claim words (the last 64 bytes of
+        # the K-split flag area) zeroed for the next launch
+        ws = ops.split_workspace(dev)
+        assert int(ws[4096 - 64:4096].cpu().count_nonzero()) == 0
 
 
 def test_ag_gemm_epochs_and_orders(dev):
@@ -141,7 +146,8 @@ def test_ag_gemm_epochs_and_orders(dev):
     flags = torch.zeros(cfg.M // 128, dtype=torch.int32, device=dev)
     counters = torch.zeros(cfg.M // 128, dtype=torch.int32, device=dev)
     outs = []
-    for epoch, seed, prod in [(1, 5, -1), (2, 6, 8), (5, 7, -1), (6, 8, -1)]:
+    for epoch, seed, prod in [(1, 5, -1), (2, 6, 8), (5, 7, -1), (6, 8, -1), (7, 9, -3), (9, 10, -3), (11, 11, -4),
+                              (12, 12, -1)]:
         _say(f"ag_gemm epoch={epoch} producers={prod}")
         A_full = torch.zeros_like(Ad)
         order = torch.from_numpy(wl.stage_order(cfg.M // 128, seed)).to(dev)
@@ -155,7 +161,7 @@ def test_ag_gemm_epochs_and_orders(dev):
 
 
 @pytest.mark.parametrize("num_cus,K,prod", [(4, 512, -1), (8, 1024, -1), (8, 1024, -2), (16, 512, -1), (3, 2048, -1),
-                                            (0, 512, -1)])
+                                            (0, 512, -1), (3, 2048, -3), (8, 1024, -3), (16, 512, -6)])
 def test_ag_gemm_cooperative_staging_capped_grid(dev, num_cus, K, prod):
     """Cooperative staging with a capped grid (every workgroup copies many
     pieces and computes several rounds of tiles): staged bytes and flags
@@ -166,7 +172,9 @@ def test_ag_gemm_cooperative_staging_capped_grid(dev, num_cus, K, prod):
     flags).  Waits are bounded so a protocol error reports instead of
     hanging.  num_cus 8 and 16 (multiples of the 8 XCDs) run the schedule in
     which the two halves of the grid take turns copying ahead (-1); -2 the
-    even share."""
+    even share; -3 and -6 the co-resident staging kernel (1 and 4 staging
+    waves per workgroup) sharing the claimed pieces with the compute
+    workgroups."""
     _say(f"ag_gemm cooperative num_cus={num_cus} K={K} producers={prod}")
     cfg, A, B, order = _ag_case(dev, K=K)
     Ad, Bd = A.to(dev), B.to(dev)
@@ -410,7 +418,7 @@ def test_gemm_split_tail_exchange_identity_exact(dev):
     assert torch.equal(ops.gemm(I, X, tile_m=256, num_cus=32).cpu(), X.cpu())
 
 
-@pytest.mark.parametrize("prod", [-1, 8])
+@pytest.mark.parametrize("prod", [-1, 8, -3])
 def test_ag_gemm_graph_replays_device_epoch(dev, prod):
     """AllGather+GEMM recorded once in a HIP graph after mk_epoch_advance,
     reading its epoch from that device word: each replay, with new shard
@@ -597,7 +605,7 @@ def test_ag_gemm_present_blocks_not_copied(dev, world, rank):
     flags = torch.zeros(nb, dtype=torch.int32, device=dev)
     counters = torch.zeros_like(flags)
     C = torch.empty((cfg.M, cfg.N), dtype=torch.bfloat16, device=dev)
-    for epoch, prod in ((1, -1), (2, -2), (3, 4)):
+    for epoch, prod in ((1, -1), (2, -2), (3, 4), (4, -3)):
         ops.ag_gemm(src.to(dev), A_full, B.to(dev), C, flags, full_order, epoch=epoch, num_producers=prod,
                     stage_counters=counters, n_present=per)
         torch.cuda.synchronize()
