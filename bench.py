@@ -189,15 +189,38 @@ def bench_rs(steps, warmup, producers, extra):
         ops.gemm_rs(A, B, work, out_pre, None, recv_pre, cfg.world, cfg.rank, flags_pub, order_d, epoch=2 ** 30,
                     num_producers=0)
 
-    r = interleaved({"rs": rs, "prestaged": prestaged, "plain": lambda i: ops.gemm(A, B, work)}, steps, warmup)
+    # the same in-launch staging with the partials arriving row block by row
+    # block (every peer's block of owned row 0, then of row 1, ...): the
+    # spread schedule folds owned row k in round k as its blocks land
+    rbs = rows // 128
+    order_rows = torch.tensor([q * rbs + rb for rb in range(rbs) for q in range(cfg.world - 1)], dtype=torch.int32,
+                              device="cuda")
+    epoch_rows = [0]
+    flags_rows = torch.zeros_like(flags)
+    counters_rows = torch.zeros_like(flags)
+
+    def rs_rows(i):
+        epoch_rows[0] += 1
+        ops.gemm_rs(A, B, work, out, peers, recv, cfg.world, cfg.rank, flags_rows, order_rows,
+                    epoch=epoch_rows[0], num_producers=producers, stage_counters=counters_rows)
+
+    r = interleaved({"rs": rs, "rs_rows": rs_rows, "prestaged": prestaged, "plain": lambda i: ops.gemm(A, B, work)},
+                    steps, warmup)
     ms, ms_plain = r["rs"], r["plain"]
     extra["gemm_rs"] = {"shape": [cfg.M, cfg.N, cfg.K], "producers": producers, "us": ms * 1e3,
                         "tflops": flops / ms / 1e9, "us_plain_gemm_same_shape": ms_plain * 1e3,
                         "us_prestaged": r["prestaged"] * 1e3, "tflops_prestaged": flops / r["prestaged"] / 1e9,
+                        "us_staged_row_block_order": r["rs_rows"] * 1e3,
+                        "overhead_prestaged": r["prestaged"] / ms_plain - 1.0,
+                        "overhead_staged_random_order": ms / ms_plain - 1.0,
+                        "overhead_staged_row_block_order": r["rs_rows"] / ms_plain - 1.0,
                         "epilogue_bytes_read": peers.numel() * 2,
-                        "note": "us: the 7 peer partials staged into recv inside the launch (cooperative copy, "
-                                "flags published as blocks land); us_prestaged: partials already in recv and "
-                                "flags published before the launch (BASELINE config 3's pre-staged partials)"}
+                        "note": "us: the 7 peer partials staged into recv inside the launch (cooperative copy "
+                                "in a seeded random block order, flags published as blocks land); "
+                                "us_staged_row_block_order: the same with the blocks arriving row block by row "
+                                "block; us_prestaged: partials already in recv and flags published before the "
+                                "launch (BASELINE config 3's pre-staged partials).  Owned row tiles are spread "
+                                "one per round in arrival order"}
 
 
 def bench_ar(steps, warmup, producers, extra):

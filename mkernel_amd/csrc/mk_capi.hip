@@ -417,7 +417,9 @@ int mk_gemm_rs(const mk_gemm_rs_args* a, void* stream) {
   p.tiles_m = (int)(a->M / bm);
   p.tiles_n = (int)(a->N / 256);
   set_grid(p, total, n_prod, p.tiles_m * p.tiles_n);
-  p.perm_mode = mk::kPermOwnedLast;
+  // Owned row tiles spread one per round, in the order their peer blocks
+  // arrive when this launch stages them.
+  p.perm_mode = mk::kPermOwnedSpread;
   p.rs_own_row0 = a->rank * own_rows;
   p.rs_own_rows = own_rows;
   p.rs_npeers = npeers;

@@ -271,6 +271,82 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_num_vgpr(32))) void stage
 }
 
 // ---------------------------------------------------------------------------
+// LDS-DMA helpers
+// ---------------------------------------------------------------------------
+
+// Raw buffer descriptor (gfx9 word 3) for inline-asm buffer instructions.
+__device__ __forceinline__ u32x4_t make_rsrc_v(const void* base, uint32_t bytes) {
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  u32x4_t r;
+  r[0] = __builtin_amdgcn_readfirstlane((uint32_t)a);
+  r[1] = __builtin_amdgcn_readfirstlane((uint32_t)(a >> 32) & 0xffffu);
+  r[2] = __builtin_amdgcn_readfirstlane(bytes);
+  r[3] = 0x00020000u;
+  return r;
+}
+
+// 16-byte buffer load straight into LDS: lane l's 16 bytes land at
+// lds_addr + 16*l.  Issued through inline asm so the compiler does not
+// serialise every later LDS read behind it; completion is tracked by hand
+// with wait_stage (vmcnt) followed by a workgroup barrier.
+// The compiler's hazard pass does not look inside inline asm, so the wait
+// states are written here: a VMEM instruction that reads an SGPR written by a
+// VALU instruction (v_readlane / v_readfirstlane, e.g. a reloaded SGPR spill)
+// needs 5 wait states, and an LDS DMA after an SALU write of M0 needs 1.
+// Without them the load can use a stale rsrc / soffset and fetch wrong bytes.
+__device__ __forceinline__ void dma16(u32x4_t r, uint32_t lds_addr, uint32_t voff, uint32_t soff) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 4\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+               :
+               : "s"(lds_addr), "v"(voff), "s"(r), "s"(soff)
+               : "memory", "m0");
+}
+
+// Two LDS DMAs in one asm statement (nothing can be scheduled between them),
+// so the 5-wait-state guard is paid once per pair.
+__device__ __forceinline__ void dma16x2(u32x4_t r, uint32_t lds0, uint32_t lds1, uint32_t v0, uint32_t v1,
+                                        uint32_t soff) {
+  asm volatile(
+      "s_mov_b32 m0, %0\n\ts_nop 4\n\tbuffer_load_dwordx4 %2, %4, %5 offen lds\n\t"
+      "s_mov_b32 m0, %1\n\ts_nop 0\n\tbuffer_load_dwordx4 %3, %4, %5 offen lds"
+      :
+      : "s"(lds0), "s"(lds1), "v"(v0), "v"(v1), "s"(r), "s"(soff)
+      : "memory", "m0");
+}
+
+// N DMAs into consecutive 1 KB LDS blocks starting at lds, paired.
+template <int N>
+__device__ __forceinline__ void dma16_run(u32x4_t r, uint32_t lds, const uint32_t (&voff)[N], uint32_t soff) {
+#pragma unroll
+  for (int i = 0; i + 1 < N; i += 2) dma16x2(r, lds + i * 1024, lds + (i + 1) * 1024, voff[i], voff[i + 1], soff);
+  if constexpr (N % 2) dma16(r, lds + (N - 1) * 1024, voff[N - 1], soff);
+}
+
+// s_waitcnt vmcnt(n) (n <= 63), other counters untouched (gfx9 encoding).
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// Wait until at most `pending` of this thread's most recent stages (L DMA
+// instructions each) are still in flight, i.e. every older stage has landed.
+template <int S, int L>
+__device__ __forceinline__ void wait_stage(int pending) {
+  static_assert(S <= 7 && (S - 1) * L < 64, "ring too deep for the waitcnt ladder");
+  if (pending >= 5 && S > 5) { wait_vm<(S > 5 ? 5 * L : 0)>(); return; }
+  if (pending >= 4 && S > 4) { wait_vm<(S > 4 ? 4 * L : 0)>(); return; }
+  if (pending >= 3 && S > 3) { wait_vm<(S > 3 ? 3 * L : 0)>(); return; }
+  if (pending >= 2 && S > 2) { wait_vm<2 * L>(); return; }
+  if (pending >= 1) { wait_vm<L>(); return; }
+  wait_vm<0>();
+}
+
+__device__ __forceinline__ bf16x4_t lds_tr4(const char* p) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
+      (__attribute__((address_space(3))) bf16x4_t*)((__attribute__((address_space(3))) char*)(p)));
+}
+
+// ---------------------------------------------------------------------------
 // Epilogue of one BM x BN tile.  acc[i][j][4a+b] is C[m][n] with
 // m = m0 + wm*WTM + 32i + ml and n (in tile) = wn*WTN + 32j + 8a + 4kg + b.
 // ---------------------------------------------------------------------------
@@ -475,82 +551,6 @@ __device__ __forceinline__ void store_tile(const GemmKParams& p, f32x16 (&acc)[C
       }
     }
   }
-}
-
-// ---------------------------------------------------------------------------
-// LDS-DMA helpers
-// ---------------------------------------------------------------------------
-
-// Raw buffer descriptor (gfx9 word 3) for inline-asm buffer instructions.
-__device__ __forceinline__ u32x4_t make_rsrc_v(const void* base, uint32_t bytes) {
-  const uint64_t a = reinterpret_cast<uint64_t>(base);
-  u32x4_t r;
-  r[0] = __builtin_amdgcn_readfirstlane((uint32_t)a);
-  r[1] = __builtin_amdgcn_readfirstlane((uint32_t)(a >> 32) & 0xffffu);
-  r[2] = __builtin_amdgcn_readfirstlane(bytes);
-  r[3] = 0x00020000u;
-  return r;
-}
-
-// 16-byte buffer load straight into LDS: lane l's 16 bytes land at
-// lds_addr + 16*l.  Issued through inline asm so the compiler does not
-// serialise every later LDS read behind it; completion is tracked by hand
-// with wait_stage (vmcnt) followed by a workgroup barrier.
-// The compiler's hazard pass does not look inside inline asm, so the wait
-// states are written here: a VMEM instruction that reads an SGPR written by a
-// VALU instruction (v_readlane / v_readfirstlane, e.g. a reloaded SGPR spill)
-// needs 5 wait states, and an LDS DMA after an SALU write of M0 needs 1.
-// Without them the load can use a stale rsrc / soffset and fetch wrong bytes.
-__device__ __forceinline__ void dma16(u32x4_t r, uint32_t lds_addr, uint32_t voff, uint32_t soff) {
-  asm volatile("s_mov_b32 m0, %0\n\ts_nop 4\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
-               :
-               : "s"(lds_addr), "v"(voff), "s"(r), "s"(soff)
-               : "memory", "m0");
-}
-
-// Two LDS DMAs in one asm statement (nothing can be scheduled between them),
-// so the 5-wait-state guard is paid once per pair.
-__device__ __forceinline__ void dma16x2(u32x4_t r, uint32_t lds0, uint32_t lds1, uint32_t v0, uint32_t v1,
-                                        uint32_t soff) {
-  asm volatile(
-      "s_mov_b32 m0, %0\n\ts_nop 4\n\tbuffer_load_dwordx4 %2, %4, %5 offen lds\n\t"
-      "s_mov_b32 m0, %1\n\ts_nop 0\n\tbuffer_load_dwordx4 %3, %4, %5 offen lds"
-      :
-      : "s"(lds0), "s"(lds1), "v"(v0), "v"(v1), "s"(r), "s"(soff)
-      : "memory", "m0");
-}
-
-// N DMAs into consecutive 1 KB LDS blocks starting at lds, paired.
-template <int N>
-__device__ __forceinline__ void dma16_run(u32x4_t r, uint32_t lds, const uint32_t (&voff)[N], uint32_t soff) {
-#pragma unroll
-  for (int i = 0; i + 1 < N; i += 2) dma16x2(r, lds + i * 1024, lds + (i + 1) * 1024, voff[i], voff[i + 1], soff);
-  if constexpr (N % 2) dma16(r, lds + (N - 1) * 1024, voff[N - 1], soff);
-}
-
-// s_waitcnt vmcnt(n) (n <= 63), other counters untouched (gfx9 encoding).
-template <int N>
-__device__ __forceinline__ void wait_vm() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
-}
-
-// Wait until at most `pending` of this thread's most recent stages (L DMA
-// instructions each) are still in flight, i.e. every older stage has landed.
-template <int S, int L>
-__device__ __forceinline__ void wait_stage(int pending) {
-  static_assert(S <= 7 && (S - 1) * L < 64, "ring too deep for the waitcnt ladder");
-  if (pending >= 5 && S > 5) { wait_vm<(S > 5 ? 5 * L : 0)>(); return; }
-  if (pending >= 4 && S > 4) { wait_vm<(S > 4 ? 4 * L : 0)>(); return; }
-  if (pending >= 3 && S > 3) { wait_vm<(S > 3 ? 3 * L : 0)>(); return; }
-  if (pending >= 2 && S > 2) { wait_vm<2 * L>(); return; }
-  if (pending >= 1) { wait_vm<L>(); return; }
-  wait_vm<0>();
-}
-
-__device__ __forceinline__ bf16x4_t lds_tr4(const char* p) {
-  return __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
-      (__attribute__((address_space(3))) bf16x4_t*)((__attribute__((address_space(3))) char*)(p)));
 }
 
 // Cursor of a workgroup's cooperative staging between tile rounds.
@@ -1214,8 +1214,8 @@ __device__ __forceinline__ void compute_role(const GemmKParams& p, int cons_id, 
 
 // Order of row tiles for a gated consumer: ascending by the stage position at
 // which the last 128-row flag of the tile is published (ties by row), so
-// compute follows arrival; for the reduce epilogue, non-owned rows first and
-// owned rows last.
+// compute follows arrival; for the reduce epilogue, the owned rows spread one
+// per round among the others.
 template <int BM, int NT>
 __device__ void build_row_perm(const GemmKParams& p, int* row_perm, int* row_key, int* scratch) {
   const int tid = threadIdx.x;
@@ -1249,15 +1249,66 @@ __device__ void build_row_perm(const GemmKParams& p, int* row_perm, int* row_key
       row_perm[rank] = i;
       row_key[rank] = key;
     }
-  } else {  // kPermOwnedLast
+  } else if (p.perm_mode == kPermOwnedSpread) {
+    // Owned row tiles spread over the order: the owned row of arrival rank k
+    // sits in segment k of nown equal segments, at offset k % L (L = the
+    // segment length), so with one segment per round every round folds one
+    // owned row and the folding workgroups rotate from round to round
+    // (reference: the device-relative slice interleave of
+    // include/operators/gemm_rs/gemm_rs.cuh:306-318).  An owned row's
+    // arrival key is the last stage position among its peers' blocks when
+    // this launch stages them (so a row-block-major stage order lets round
+    // k fold the k-th row), else its index.
     const int own0 = p.rs_own_row0 / BM, nown = p.rs_own_rows / BM;
+    const int per = BM / kFlagRows, rbs = p.rs_own_rows / kFlagRows;
+    const bool staged = p.st_nblocks > 0 && (p.st_coop || p.n_prod > 0);
+    int* pos = scratch;                        // flag -> stage position
+    int* okey = scratch + p.st_nblocks;        // owned row -> arrival key
+    int* oby = okey + nown;                    // arrival rank -> owned row
+    if (staged) {
+      for (int i = tid; i < p.st_nblocks; i += NT) {
+        const int f = p.st_order ? p.st_order[i] : i;
+        if ((unsigned)f < (unsigned)p.st_nblocks) pos[f] = i;
+      }
+    }
+    __syncthreads();
+    for (int k = tid; k < nown; k += NT) {
+      int key = k;
+      if (staged) {
+        key = 0;
+        for (int q = 0; q < p.rs_npeers; ++q)
+          for (int sub = 0; sub < per; ++sub) key = max(key, pos[q * rbs + k * per + sub]);
+      }
+      okey[k] = key;
+    }
+    __syncthreads();
+    for (int k = tid; k < nown; k += NT) {
+      int rank = 0;
+      for (int j = 0; j < nown; ++j) rank += (okey[j] < okey[k]) || (okey[j] == okey[k] && j < k);
+      oby[rank] = k;
+    }
+    __syncthreads();
+    const int L = max(tm / max(nown, 1), 1);
+    auto seg_start = [&](int k) { return (int)((int64_t)k * tm / nown); };
     for (int i = tid; i < tm; i += NT) {
-      int r;
-      if (i < tm - nown) r = i < own0 ? i : i + nown;
-      else r = own0 + (i - (tm - nown));
+      int r, key = -1;
+      if (nown == 0) {
+        r = i;
+      } else {
+        int k = (int)((int64_t)i * nown / tm);
+        while (k + 1 < nown && seg_start(k + 1) <= i) ++k;
+        while (k > 0 && seg_start(k) > i) --k;
+        const int slot = seg_start(k) + k % L;
+        if (i == slot) {
+          r = own0 + oby[k];
+          key = staged ? okey[oby[k]] : -1;
+        } else {
+          const int j = i - k - (i > slot ? 1 : 0);  // index among the non-owned rows
+          r = j < own0 ? j : j + nown;
+        }
+      }
       row_perm[i] = r;
-      // the owned rows need every staged peer block, the others none
-      row_key[i] = (r >= own0 && r < own0 + nown) ? p.st_nblocks - 1 : -1;
+      row_key[i] = key;
     }
   }
   __syncthreads();
@@ -1455,17 +1506,17 @@ static hipError_t launch_t(const GemmKParams& p, hipStream_t stream) {
   // threads that both find the flag clear both set the attribute, which is
   // harmless; a launch never runs before its device's attribute is set.
   static PerDeviceFlag attr_set;
+  constexpr uint32_t lds = C::LDS_BYTES;
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return e;
   if (!attr_set.is_set(dev)) {
     e = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_kernel<BM, WAVES, EPI, BN>),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, C::LDS_BYTES);
+                            hipFuncAttributeMaxDynamicSharedMemorySize, lds);
     if (e != hipSuccess) return e;
     attr_set.set(dev);
   }
-  hipLaunchKernelGGL((gemm_kernel<BM, WAVES, EPI, BN>), dim3(p.n_prod + p.n_cons), dim3(C::NT), C::LDS_BYTES,
-                     stream, p);
+  hipLaunchKernelGGL((gemm_kernel<BM, WAVES, EPI, BN>), dim3(p.n_prod + p.n_cons), dim3(C::NT), lds, stream, p);
   return hipGetLastError();
 }
 
@@ -1508,8 +1559,9 @@ hipError_t launch_gemm_costaged(const GemmKParams& p, int epi, int n_stage_waves
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return e;
+  const uint32_t lds = C::LDS_BYTES;
   if (!flag.is_set(dev)) {
-    e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, C::LDS_BYTES);
+    e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
     if (e != hipSuccess) return e;
     flag.set(dev);
   }
@@ -1534,7 +1586,7 @@ hipError_t launch_gemm_costaged(const GemmKParams& p, int epi, int n_stage_waves
   if ((e = hipEventRecord(cs->join, cs->side)) != hipSuccess) return e;
   GemmKParams pk = pg;
   void* args[] = {&pk};
-  if ((e = hipLaunchKernel(fn, dim3(p.n_prod + p.n_cons), dim3(C::NT), args, C::LDS_BYTES, stream)) != hipSuccess)
+  if ((e = hipLaunchKernel(fn, dim3(p.n_prod + p.n_cons), dim3(C::NT), args, lds, stream)) != hipSuccess)
     return e;
   return hipStreamWaitEvent(stream, cs->join, 0);
 }

@@ -7,7 +7,7 @@
 namespace mk {
 
 enum Epilogue : int { kEpiStore = 0, kEpiSwiGLU = 1, kEpiReduce = 2 };
-enum PermMode : int { kPermNone = 0, kPermArrival = 1, kPermOwnedLast = 2, kPermPeerArrival = 3 };
+enum PermMode : int { kPermNone = 0, kPermArrival = 1, kPermOwnedSpread = 2, kPermPeerArrival = 3 };
 constexpr int kMaxTilesM = 512;
 constexpr int kMaxSplitListTiles = 4096;  // K-split with a permuted tile order: at most this many tiles
 constexpr int kMaxRounds = 64;   // cooperative staging between rounds: at most this many rounds

@@ -255,6 +255,43 @@ def test_gemm_rs_vs_oracle(dev, rank, producers, num_cus, K):
         assert torch.equal(recv.cpu(), peers)
 
 
+@pytest.mark.parametrize("world,rank,M,num_cus", [(8, 3, 4096, 0), (4, 0, 2048, 8), (8, 7, 4096, 16), (2, 1, 1024, 0)])
+def test_gemm_rs_spread_schedule_orders(dev, world, rank, M, num_cus):
+    """Owned row tiles run one per round in the arrival order of their peer
+    blocks: with the partials staged inside the launch in a row-block-major
+    order, in a random order, and pre-staged with published flags, the owned
+    slice and the sends are bit-identical (each owned element is the same
+    fp32 sum in rank order whatever round folds it), and match the oracle."""
+    _say(f"gemm_rs spread world={world} rank={rank} M={M} num_cus={num_cus}")
+    cfg = wl.RsCfg(world=world, rank=rank, M=M, K=256, N=512)
+    A, B, peers, order = wl.rs_inputs(cfg)
+    rows = cfg.M // cfg.world
+    rbs = rows // 128
+    Ad, Bd, pd = A.to(dev), B.to(dev), peers.to(dev)
+    nfl = (world - 1) * rbs
+    row_major = torch.tensor([q * rbs + rb for rb in range(rbs) for q in range(world - 1)], dtype=torch.int32)
+    results = []
+    for mode, od in (("rows", row_major), ("random", torch.from_numpy(order)), ("prestaged", None)):
+        work = torch.zeros((cfg.M, cfg.N), dtype=torch.bfloat16, device=dev)
+        out = torch.zeros((rows, cfg.N), dtype=torch.bfloat16, device=dev)
+        counters = torch.zeros(nfl, dtype=torch.int32, device=dev)
+        if mode == "prestaged":
+            ops.gemm_rs(Ad, Bd, work, out, None, pd.clone(), world, rank, torch.full((nfl,), 5, dtype=torch.int32,
+                        device=dev), torch.from_numpy(order).to(dev), epoch=5, num_producers=0, num_cus=num_cus)
+        else:
+            recv = torch.zeros_like(pd)
+            ops.gemm_rs(Ad, Bd, work, out, pd, recv, world, rank, torch.zeros(nfl, dtype=torch.int32, device=dev),
+                        od.to(dev), epoch=5, num_producers=-1, stage_counters=counters, num_cus=num_cus)
+            torch.cuda.synchronize()
+            assert torch.equal(recv.cpu(), peers)
+        torch.cuda.synchronize()
+        results.append((work.cpu(), out.cpu()))
+    for w, o in results[1:]:
+        assert torch.equal(w, results[0][0]) and torch.equal(o, results[0][1])
+    _, owned = gemm_rs_ref(A, B, peers, rank, world)
+    assert rel_fro(results[0][1].float(), owned) < TOL
+
+
 def test_gemm_rs_equal_partials_known_answer(dev):
     """All 8 partials equal => output is exactly 8x the partial.  Integer
     operands in {-1, 0, 1} make every partial an exact small integer."""
