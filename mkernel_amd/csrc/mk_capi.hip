@@ -271,7 +271,13 @@ int mk_gemm(const mk_gemm_args* a, void* stream) {
   return e == hipSuccess ? MK_OK : hip_fail(e, "mk_gemm launch");
 }
 
-int mk_ag_gemm(const mk_ag_gemm_args* a, void* stream) {
+}  // extern "C"
+
+namespace {
+// Validates mk_ag_gemm's arguments and fills the launch: every refusal
+// happens here, before anything is queued.  *costage_waves > 0 selects the
+// co-resident staging kernel (that many one-wave workgroups).
+int prepare_ag(const mk_ag_gemm_args* a, void* stream, mk::GemmKParams& p, int* costage_out) {
   if (!a || !a->A_full || !a->B || !a->C) return fail(MK_EINVAL, "mk_ag_gemm: null argument");
   DevInfo d;
   if (int rc = device_info(&d)) return rc;
@@ -312,7 +318,6 @@ int mk_ag_gemm(const mk_ag_gemm_args* a, void* stream) {
     return fail(MK_EINVAL, "mk_ag_gemm: n_present=%d must be in [0, M/128]", a->n_present);
   if (a->n_present > 0 && !a->stage_order)
     return fail(MK_EINVAL, "mk_ag_gemm: n_present needs stage_order (the present blocks are its first entries)");
-  mk::GemmKParams p;
   fill_common(p);
   p.A = static_cast<const uint16_t*>(a->A_full);
   p.B = static_cast<const uint16_t*>(a->B);
@@ -348,11 +353,26 @@ int mk_ag_gemm(const mk_ag_gemm_args* a, void* stream) {
   }
   if (int rc = check_ws(a->split_ws, a->split_ws_bytes, "mk_ag_gemm")) return rc;
   plan_split(p, bm, a->split_ws, a->split_ws_bytes);
-  hipError_t e = costage_waves ? mk::launch_gemm_costaged(p, mk::kEpiStore, costage_waves * total,
-                                                          static_cast<hipStream_t>(stream))
-                               : mk::launch_gemm(p, bm, mk::kEpiStore, static_cast<hipStream_t>(stream));
+  *costage_out = costage_waves * total;
+  return MK_OK;
+}
+
+int launch_ag(const mk::GemmKParams& p, int costage, void* stream) {
+  hipError_t e = costage ? mk::launch_gemm_costaged(p, mk::kEpiStore, costage, static_cast<hipStream_t>(stream))
+                         : mk::launch_gemm(p, 256, mk::kEpiStore, static_cast<hipStream_t>(stream));
   return e == hipSuccess ? MK_OK : hip_fail(e, "mk_ag_gemm launch");
 }
+}  // namespace
+
+extern "C" {
+
+int mk_ag_gemm(const mk_ag_gemm_args* a, void* stream) {
+  mk::GemmKParams p;
+  int costage = 0;
+  if (int rc = prepare_ag(a, stream, p, &costage)) return rc;
+  return launch_ag(p, costage, stream);
+}
+
 
 int mk_ag_gemm_noalloc(const mk_ag_gemm_args* a, void* stream) {
   if (!a) return fail(MK_EINVAL, "mk_ag_gemm_noalloc: null argument");
@@ -370,6 +390,13 @@ int mk_ag_gemm_noalloc(const mk_ag_gemm_args* a, void* stream) {
   b.split_ws = base;
   b.split_ws_bytes = kNoAllocSplitBytes;  // a tail split needing more partial tiles is not made
   b.stage_counters = reinterpret_cast<uint32_t*>(static_cast<char*>(base) + kNoAllocSplitBytes);
+  // the co-resident staging kernel would need a side stream and events,
+  // which the library creates on first use: stage cooperatively instead
+  if (b.num_producers <= -3) b.num_producers = -1;
+  // every argument check before anything is queued on the stream
+  mk::GemmKParams p;
+  int costage = 0;
+  if (int rc = prepare_ag(&b, stream, p, &costage)) return rc;
   const int n_counters = (int)(a->M / 128);
   const int n_flags = (int)(kSplitFlagBytes / 4);
   const int n = std::max(n_flags, n_counters);
@@ -377,7 +404,7 @@ int mk_ag_gemm_noalloc(const mk_ag_gemm_args* a, void* stream) {
                      static_cast<uint32_t*>(base), n_flags, b.stage_counters, n_counters);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return hip_fail(e, "mk_ag_gemm_noalloc scratch clear");
-  return mk_ag_gemm(&b, stream);
+  return launch_ag(p, costage, stream);
 }
 
 int64_t mk_ag_gemm_noalloc_scratch_bytes(void) { return kNoAllocBytes; }

@@ -797,9 +797,31 @@ __device__ __forceinline__ void compute_role(const GemmKParams& p, int cons_id, 
       // together.  The host sets this only with rb_expert.
       const int rt = __builtin_amdgcn_readfirstlane(t / p.tiles_n);
       const int e = __builtin_amdgcn_readfirstlane(p.rb_expert[rt]);
+      // Run bounds 64 row tiles per step: every lane loads one table entry
+      // and a ballot finds the first entry of another expert, so a long run
+      // (a hot expert) costs one load per 64 tiles, not one per tile.
+      const int ln = threadIdx.x & 63;
       int r0 = rt, r1 = rt + 1;
-      while (r0 > 0 && __builtin_amdgcn_readfirstlane(p.rb_expert[r0 - 1]) == e) --r0;
-      while (r1 < tiles_m && __builtin_amdgcn_readfirstlane(p.rb_expert[r1]) == e) ++r1;
+      for (;;) {  // backwards: r0 = one past the last other-expert entry below rt
+        const int idx = r0 - 1 - ln;
+        const uint64_t other = __ballot(idx < 0 || p.rb_expert[max(idx, 0)] != e);
+        if (other) {
+          r0 -= __builtin_ctzll(other);  // entries r0-1 .. r0-k share e, entry r0-1-k does not
+          break;
+        }
+        r0 -= 64;
+      }
+      for (;;) {  // forwards: r1 = the first other-expert entry at or above rt + 1
+        const int idx = r1 + ln;
+        const uint64_t other = __ballot(idx >= tiles_m || p.rb_expert[min(idx, tiles_m - 1)] != e);
+        if (other) {
+          r1 += __builtin_ctzll(other);
+          break;
+        }
+        r1 += 64;
+      }
+      r0 = __builtin_amdgcn_readfirstlane(r0);
+      r1 = __builtin_amdgcn_readfirstlane(r1);
       const int local = t - r0 * p.tiles_n, nr = r1 - r0;
       tn = local / nr;
       tm = r0 + local % nr;

@@ -299,7 +299,7 @@ def _ag_module():
 
     def ag_gemm_multinode(A, B, C, barrier, recv_buf_ptr, fifo_triggers, fifo_head, fifo_tail, fifo_tail_cache,
                           fifo_capacity, arrival_flags_ptr, epoch, node_idx, num_comm_sms, a_half_bytes, A_recv,
-                          active_sms=0, num_intra_comm_override=0, num_nodes=1, *, peer_shards=None,
+                          active_sms=132, num_intra_comm_override=0, num_nodes=1, *, peer_shards=None,
                           stage_order=None, dedicated_producers=0):
         """C = A_gathered @ B (reference include/operators/ag_gemm/ag_gemm.cuh:362-509).
 
@@ -320,8 +320,13 @@ def _ag_module():
         ``num_intra_comm_override`` / ``num_comm_sms`` (the reference's SM
         split) select nothing: the blocks are staged cooperatively by the
         compute workgroups, unless ``dedicated_producers`` > 0 asks for that
-        many producer workgroups.  ``active_sms`` caps the grid (0 or >= the
-        CU count: every CU)."""
+        many producer workgroups.  ``active_sms`` caps the persistent grid
+        at that many workgroups (0 or >= the CU count: every CU).  Its
+        default is the reference's, 132 (include/operators/ag_gemm/
+        session.cuh:227), so a call that relies on it runs on 132 of the
+        MI355X's 256 CUs, as it runs on 132 SMs on any reference GPU; the
+        reference benches pass the device's full count
+        (bench/ag_gemm_bench.py:375-376)."""
         _single_node(num_nodes)
         s.epoch = int(epoch)
         Af = _data(A)
@@ -477,13 +482,14 @@ def _ar_module():
 
 # ---------------------------------------------------------------- MoE ----
 def _local_tables(s: _Session, pre_tokens, pull, padded, n_experts: int, R_pad: int, node_idx: int,
-                  num_nodes) -> torch.Tensor:
+                  num_nodes, validate: bool = True) -> torch.Tensor:
     """Checks that the routing tables describe one GPU's layout (every pulled
     token is on this GPU) and returns the per-local-expert padded row counts.
     The reference's padded table lists every expert of the job
     (bench/dispatch_gemm_bench.py:161-166,280); the local slice starts at
     this GPU's first expert.  Table contents are checked once per tensor
-    version (one host read-back)."""
+    version (one host read-back, which synchronizes the stream);
+    ``validate=False`` skips that check."""
     _single_node(num_nodes)
     rank, world = _place(pre_tokens)
     if world != 1 or int(node_idx) != 0:
@@ -497,7 +503,7 @@ def _local_tables(s: _Session, pre_tokens, pull, padded, n_experts: int, R_pad: 
     else:
         raise ValueError(f"padded_tokens_per_expert has {padded.numel()} entries for {n_experts} local experts")
     key = ("tables", str(dev), pull.data_ptr(), pull._version, padded.data_ptr(), padded._version, R_pad)
-    if not s.checked(key):
+    if validate and not s.checked(key):
         p = pull[:R_pad].cpu().numpy()
         real = p[:, 0] >= 0
         bad = None
@@ -519,7 +525,7 @@ def _dispatch_module():
                                 sync_barrier, recv_buf_ptr, fifo_triggers, fifo_head, fifo_tail, fifo_tail_cache,
                                 fifo_capacity, arrival_flags_ptr, epoch, node_idx, num_local_tokens,
                                 num_padded_local_tokens, num_send_sms, num_copy_sms, num_comm_sms_intra,
-                                num_nodes=1, *, write_post_tokens=False):
+                                num_nodes=1, *, write_post_tokens=False, validate_tables=True):
         """Token dispatch + grouped GEMM (reference
         include/operators/dispatch_gemm/dispatch_gemm.cuh:238-387).
 
@@ -530,11 +536,14 @@ def _dispatch_module():
         reference's dispatch_gemm fusion); ``post_tokens`` (the permuted
         copy) is written only with ``write_post_tokens=True`` — the
         reference bench checks ``outputs`` only
-        (bench/dispatch_gemm_bench.py:463-487)."""
+        (bench/dispatch_gemm_bench.py:463-487).  ``validate_tables=False``
+        skips the once-per-table-version host check of the tables (a
+        read-back that synchronizes the stream)."""
         tok = _data(pre_tokens)[:num_local_tokens]
         Rp = int(num_padded_local_tokens)
         E = weights.shape[0]
-        pl = _local_tables(s, pre_tokens, pull_dispatch_indices, padded_tokens_per_expert, E, Rp, node_idx, num_nodes)
+        pl = _local_tables(s, pre_tokens, pull_dispatch_indices, padded_tokens_per_expert, E, Rp, node_idx, num_nodes,
+                           validate_tables)
         if Rp == 0:
             return outputs
         pull = pull_dispatch_indices[:Rp]
@@ -560,8 +569,8 @@ def _glu_module():
                                             fifo_triggers, fifo_head, fifo_tail, fifo_tail_cache, fifo_capacity,
                                             arrival_flags_ptr, epoch, node_idx, num_local_tokens,
                                             num_padded_local_tokens, num_send_sms, num_copy_sms, num_comm_sms_intra,
-                                            use_gather, num_nodes=1, cross_node_barrier_ptr=0, *,
-                                            write_post_tokens=False):
+                                            use_gather, num_nodes, cross_node_barrier_ptr=0, *,
+                                            write_post_tokens=False, validate_tables=True):
         """Dispatch -> GEMM1 + SwiGLU -> GEMM2 -> top-k weighted combine
         (reference include/operators/dispatch_gemm_glu_combine/dispatch_gemm_glu_combine.cuh:307-548).
 
@@ -577,17 +586,20 @@ def _glu_module():
         tables on every call (two small launches into session-owned
         buffers: the tables may change between calls); the one-GPU layout
         check (every row owned by this GPU, every slot inside the CSR) runs
-        once per table version."""
+        once per table version, as a host read-back that synchronizes the
+        stream; ``validate_tables=False`` skips it (the slot inversion still
+        bounds-checks every slot on the device)."""
         tok = _data(pre_tokens)[:num_local_tokens]
         yo = _data(y_out)
         Rp = int(num_padded_local_tokens)
         T = int(num_local_tokens)
         E = w1.shape[0]
         dev = yo.device
-        pl = _local_tables(s, pre_tokens, pull_dispatch_indices, padded_tokens_per_expert, E, Rp, node_idx, num_nodes)
+        pl = _local_tables(s, pre_tokens, pull_dispatch_indices, padded_tokens_per_expert, E, Rp, node_idx, num_nodes,
+                           validate_tables)
         key = ("csr", str(dev), owner_offset.data_ptr(), owner_offset._version, row_to_owner.data_ptr(),
                row_to_owner._version, row_to_slot.data_ptr(), row_to_slot._version, Rp, T)
-        if not s.checked(key):
+        if validate_tables and not s.checked(key):
             owners = row_to_owner[:Rp].cpu().numpy()
             slots = row_to_slot[:Rp].cpu().numpy()
             nslots = int(owner_offset[T].item())

@@ -45,7 +45,11 @@ def split_workspace(device=None, stream=None) -> torch.Tensor:
     Graph capture runs on a stream of its own: fetch the workspace before
     capturing and pass it as ``split_ws``; one first created inside the
     capture has its zero-fill recorded into the graph (about 11 us per
-    replay on MI355X)."""
+    replay on MI355X).  Every distinct (device, stream handle) keeps its
+    workspace (mk_query_workspace_bytes() bytes, ~67 MB on 256 CUs) until
+    the process exits or release_split_workspaces() is called; a stream
+    created later with a recycled handle reuses that entry, which is safe
+    because each launch leaves the workspace zeroed."""
     dev = torch.device("cuda", torch.cuda.current_device() if device is None else torch.device(device).index or 0)
     if stream is None:
         stream = torch.cuda.current_stream(dev)
@@ -58,6 +62,14 @@ def split_workspace(device=None, stream=None) -> torch.Tensor:
         ws = torch.zeros(n, dtype=torch.uint8, device=dev)
         _split_ws[key] = ws
     return ws
+
+
+def release_split_workspaces() -> None:
+    """Free every cached default K-split workspace (after synchronizing
+    every device that has one, so no queued launch still uses them)."""
+    for dev in {k[0] for k in _split_ws}:
+        torch.cuda.synchronize(dev)
+    _split_ws.clear()
 
 
 def _ws(split_ws, device) -> tuple:

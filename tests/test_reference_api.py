@@ -45,6 +45,28 @@ REF_ARGS = {
 }
 
 
+# Default values the reference's pybind blocks give (include/operators/
+# ag_gemm/session.cuh:227-228, dispatch_gemm_glu_combine/session.cuh:154).
+# A required reference argument after defaulted ones (ag_gemm's num_nodes)
+# needs a default in Python; it is not listed.
+REF_DEFAULTS = {
+    ("ag_gemm", "ag_gemm_multinode"): {"active_sms": 132, "num_intra_comm_override": 0},
+    ("dispatch_gemm_glu_combine", "moe_dispatch_gemm_glu_combine_fused"): {"cross_node_barrier_ptr": 0},
+}
+
+
+@pytest.mark.parametrize("mod,fn", sorted(REF_DEFAULTS))
+def test_reference_argument_defaults(mod, fn):
+    sig = inspect.signature(getattr(load_module.load(mod), fn))
+    for name, value in REF_DEFAULTS[(mod, fn)].items():
+        assert sig.parameters[name].default == value, name
+    # every other reference argument before the first defaulted one is required
+    ref = REF_ARGS[(mod, fn)]
+    first = min(ref.index(n) for n in REF_DEFAULTS[(mod, fn)])
+    for name in ref[:first]:
+        assert sig.parameters[name].default is inspect.Parameter.empty, name
+
+
 @pytest.mark.parametrize("mod,fn", sorted(REF_ARGS))
 def test_reference_argument_lists(mod, fn):
     m = load_module.load(mod)
