@@ -168,7 +168,8 @@ typedef struct mk_gemm_rs_args {
   const int32_t* stage_order;   /* [(world-1) * (M/world)/128]; NULL = ascending */
   uint32_t epoch;
   int32_t gated;
-  int32_t num_producers;        /* as in mk_ag_gemm; -1 and -2 = cooperative staging, even share */
+  int32_t num_producers;        /* as in mk_ag_gemm; -1 and -2 = cooperative staging, even share;
+                                   <= -3 = co-resident staging kernel (needs split_ws) */
   int32_t num_cus;
   uint32_t spin_limit;
   uint32_t* error_word;
@@ -212,7 +213,8 @@ typedef struct mk_gemm_ar_args {
   const int32_t* stage_order;   /* [(world-1) * M/128]; NULL = ascending, no arrival order */
   uint32_t epoch;
   int32_t gated;
-  int32_t num_producers;        /* as in mk_ag_gemm; -1 and -2 = cooperative staging, even share */
+  int32_t num_producers;        /* as in mk_ag_gemm; -1 and -2 = cooperative staging, even share;
+                                   <= -3 = co-resident staging kernel (needs split_ws) */
   int32_t num_cus;
   uint32_t spin_limit;
   uint32_t* error_word;

@@ -140,6 +140,26 @@ int check_ws(const void* ws, int64_t bytes, const char* fn) {
   return MK_OK;
 }
 
+// num_producers <= -3 asks for the co-resident staging kernel with
+// -2 - num_producers one-wave workgroups per CU (1..4).  Under graph capture
+// the fork/join would become two graph branches whose order the replay does
+// not fix, so the launch stages cooperatively instead (*waves = 0).
+int costage_request(int gated, int num_producers, const void* split_ws, int64_t split_ws_bytes, void* stream,
+                    const char* fn, int* waves) {
+  *waves = (gated && num_producers <= -3) ? -2 - num_producers : 0;
+  if (!*waves) return MK_OK;
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  hipError_t ce = hipStreamIsCapturing(static_cast<hipStream_t>(stream), &cap);
+  if (ce != hipSuccess) return hip_fail(ce, "hipStreamIsCapturing");
+  if (cap != hipStreamCaptureStatusNone) {
+    *waves = 0;
+    return MK_OK;
+  }
+  if (!split_ws || split_ws_bytes < kSplitFlagBytes)
+    return fail(MK_EINVAL, "%s: co-resident staging keeps its claim word in split_ws, which is NULL or short", fn);
+  return MK_OK;
+}
+
 }  // namespace
 
 namespace mk {
@@ -298,17 +318,10 @@ int prepare_ag(const mk_ag_gemm_args* a, void* stream, mk::GemmKParams& p, int* 
   const bool coop = a->gated && a->num_producers < 0;
   // num_producers <= -3: co-resident staging kernel, -2 - num_producers
   // one-wave workgroups per CU beside the GEMM
-  int costage_waves = (a->gated && a->num_producers <= -3) ? -2 - a->num_producers : 0;
-  if (costage_waves) {
-    // Under graph capture the fork/join would become two graph branches
-    // whose order the replay does not fix; stage cooperatively instead.
-    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
-    hipError_t ce = hipStreamIsCapturing(static_cast<hipStream_t>(stream), &cap);
-    if (ce != hipSuccess) return hip_fail(ce, "mk_ag_gemm hipStreamIsCapturing");
-    if (cap != hipStreamCaptureStatusNone) costage_waves = 0;
-  }
-  if (costage_waves && (!a->split_ws || a->split_ws_bytes < kSplitFlagBytes))
-    return fail(MK_EINVAL, "mk_ag_gemm: co-resident staging keeps its claim word in split_ws, which is NULL or short");
+  int costage_waves = 0;
+  if (int rc = costage_request(a->gated, a->num_producers, a->split_ws, a->split_ws_bytes, stream, "mk_ag_gemm",
+                               &costage_waves))
+    return rc;
   if (coop && !a->stage_counters) return fail(MK_EINVAL, "mk_ag_gemm: cooperative staging needs stage_counters");
   int total;
   if (int rc = grid_total(a->num_cus, d, "mk_ag_gemm", &total)) return rc;
@@ -424,8 +437,12 @@ int mk_gemm_rs(const mk_gemm_rs_args* a, void* stream) {
   const int own_rows = (int)(a->M / a->world);
   int total;
   if (int rc = grid_total(a->num_cus, d, "mk_gemm_rs", &total)) return rc;
-  if (a->num_producers < -2) return fail(MK_EINVAL, "mk_gemm_rs: num_producers must be >= -2");
+  if (a->num_producers < -6) return fail(MK_EINVAL, "mk_gemm_rs: num_producers must be >= -6");
   const bool coop = a->gated && npeers > 0 && a->num_producers < 0;
+  int costage_waves = 0;
+  if (int rc = costage_request(a->gated && npeers > 0, a->num_producers, a->split_ws, a->split_ws_bytes, stream,
+                               "mk_gemm_rs", &costage_waves))
+    return rc;
   const int n_prod = (a->gated && npeers > 0 && a->num_producers > 0) ? a->num_producers : 0;
   if (a->gated && npeers > 0) {
     if (!a->flags) return fail(MK_EINVAL, "mk_gemm_rs: gated launch needs flags");
@@ -466,13 +483,18 @@ int mk_gemm_rs(const mk_gemm_rs_args* a, void* stream) {
       p.st_order = a->stage_order;
       p.st_flags = a->flags;
       p.st_counters = a->stage_counters;
-      p.st_coop = coop ? 1 : 0;  // even share (measured faster here than alternating halves)
+      // even share (measured faster here than alternating halves); <= -3: claimed
+      p.st_coop = costage_waves ? 3 : coop ? 1 : 0;
       p.st_batch = 8;
+      if (costage_waves)
+        p.st_claim = reinterpret_cast<uint32_t*>(static_cast<char*>(a->split_ws) + kClaimOffset);
     }
   }
   if (int rc = check_ws(a->split_ws, a->split_ws_bytes, "mk_gemm_rs")) return rc;
   plan_split(p, bm, a->split_ws, a->split_ws_bytes);
-  hipError_t e = mk::launch_gemm(p, bm, mk::kEpiReduce, static_cast<hipStream_t>(stream));
+  hipError_t e = costage_waves ? mk::launch_gemm_costaged(p, mk::kEpiReduce, costage_waves * total,
+                                                          static_cast<hipStream_t>(stream))
+                               : mk::launch_gemm(p, bm, mk::kEpiReduce, static_cast<hipStream_t>(stream));
   return e == hipSuccess ? MK_OK : hip_fail(e, "mk_gemm_rs launch");
 }
 
@@ -491,9 +513,13 @@ int mk_gemm_ar(const mk_gemm_ar_args* a, void* stream) {
     return fail(MK_ESHAPE, "mk_gemm_ar: too many flags for the arrival-order schedule");
   int total;
   if (int rc = grid_total(a->num_cus, d, "mk_gemm_ar", &total)) return rc;
-  if (a->num_producers < -2) return fail(MK_EINVAL, "mk_gemm_ar: num_producers must be >= -2");
+  if (a->num_producers < -6) return fail(MK_EINVAL, "mk_gemm_ar: num_producers must be >= -6");
   const bool gated = a->gated && npeers > 0;
   const bool coop = gated && a->num_producers < 0;
+  int costage_waves = 0;
+  if (int rc = costage_request(gated, a->num_producers, a->split_ws, a->split_ws_bytes, stream, "mk_gemm_ar",
+                               &costage_waves))
+    return rc;
   const int n_prod = (gated && a->num_producers > 0) ? a->num_producers : 0;
   if (gated) {
     if (!a->flags) return fail(MK_EINVAL, "mk_gemm_ar: gated launch needs flags");
@@ -537,13 +563,18 @@ int mk_gemm_ar(const mk_gemm_ar_args* a, void* stream) {
       p.st_order = a->stage_order;
       p.st_flags = a->flags;
       p.st_counters = a->stage_counters;
-      p.st_coop = coop ? 1 : 0;  // even share (measured faster here than alternating halves)
+      // even share (measured faster here than alternating halves); <= -3: claimed
+      p.st_coop = costage_waves ? 3 : coop ? 1 : 0;
       p.st_batch = 8;
+      if (costage_waves)
+        p.st_claim = reinterpret_cast<uint32_t*>(static_cast<char*>(a->split_ws) + kClaimOffset);
     }
   }
   if (int rc = check_ws(a->split_ws, a->split_ws_bytes, "mk_gemm_ar")) return rc;
   plan_split(p, bm, a->split_ws, a->split_ws_bytes);
-  hipError_t e = mk::launch_gemm(p, bm, mk::kEpiReduce, static_cast<hipStream_t>(stream));
+  hipError_t e = costage_waves ? mk::launch_gemm_costaged(p, mk::kEpiReduce, costage_waves * total,
+                                                          static_cast<hipStream_t>(stream))
+                               : mk::launch_gemm(p, bm, mk::kEpiReduce, static_cast<hipStream_t>(stream));
   return e == hipSuccess ? MK_OK : hip_fail(e, "mk_gemm_ar launch");
 }
 

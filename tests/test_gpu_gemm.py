@@ -225,7 +225,8 @@ def test_ag_gemm_bounded_wait_reports_timeout(dev):
 
 
 @pytest.mark.parametrize("rank,producers,num_cus,K", [(0, 4, 0, 256), (3, 8, 0, 256), (7, 0, 0, 256), (5, -1, 0, 256),
-                                                     (2, -1, 4, 1024), (6, -1, 3, 256), (1, -1, 5, 2048)])
+                                                     (2, -1, 4, 1024), (6, -1, 3, 256), (1, -1, 5, 2048),
+                                                     (4, -3, 0, 256), (3, -4, 8, 512)])
 def test_gemm_rs_vs_oracle(dev, rank, producers, num_cus, K):
     _say(f"gemm_rs rank={rank} producers={producers} num_cus={num_cus} K={K}")
     cfg = wl.RsCfg(world=8, rank=rank, M=2048, K=K, N=512)
@@ -312,7 +313,8 @@ def test_gemm_rs_equal_partials_known_answer(dev):
 
 
 @pytest.mark.parametrize("producers,num_cus,M,N,K", [(-1, 0, 1024, 512, 256), (4, 0, 1024, 512, 256),
-                                                     (-1, 6, 2048, 768, 512), (0, 0, 512, 512, 128)])
+                                                     (-1, 6, 2048, 768, 512), (0, 0, 512, 512, 128),
+                                                     (-3, 0, 1024, 512, 256), (-6, 16, 2048, 768, 512)])
 def test_gemm_ar_vs_oracle(dev, producers, num_cus, M, N, K):
     """GEMM + all-reduce: C_final = A@B + sum of 7 staged peer partials over
     all rows; staged bytes exact, every output tile published with the
