@@ -343,7 +343,10 @@ def bench_moe(steps, warmup, extra):
     extra["moe_dispatch_gemm1"] = {"R": R, "R_pad": R_pad, "experts_used": int(used.sum()), "us": ms4 * 1e3,
                                    "tflops": f4 / ms4 / 1e9, "us_permute_then_gemm1": ms4_unfused * 1e3,
                                    "us_permute": ms_perm * 1e3,
-                                   "permute_GBs": 2 * R_pad * cfg.H * 2 / ms_perm / 1e6}
+                                   # the R routed rows read once, all R_pad rows written
+                                   # (padding rows as zeros); the padding rows are not read
+                                   "permute_GBs": (R + R_pad) * cfg.H * 2 / ms_perm / 1e6,
+                                   "permute_bytes": (R + R_pad) * cfg.H * 2}
     extra["moe_ffn_combine"] = {"us": ms5 * 1e3, "tokens_per_s": cfg.tokens / ms5 * 1e3, "tflops": f5 / ms5 / 1e9,
                                 "us_with_separate_permute": ms5_unfused * 1e3,
                                 "us_tile_128x256": r5["fused_tile256"] * 1e3,
@@ -440,17 +443,19 @@ def cpu_baseline(A_full, B, rows: int = 256, reps: int = 3):
 
 
 def load_traffic():
-    """(bytes, source) of the headline kernel's HBM traffic per launch, read
-    from profiles/traffic.json (rocprofv3 --pmc FETCH_SIZE + WRITE_SIZE,
-    scaled by the copy-kernel calibration; not measured in this run: the
-    counters need their own profiler runs), or (None, None)."""
+    """(bytes, source) of the headline kernel's memory traffic per launch,
+    read from profiles/traffic.json (rocprofv3 --pmc: the L2's DRAM-destined
+    read requests in 32-byte units and its 64-byte write requests,
+    calibrated on a copy kernel; the 256 MB MALL serves part of these reads
+    and no counter separates them; not measured in this run: the counters
+    need their own profiler runs), or (None, None)."""
     path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "traffic.json")
     try:
         with open(path) as f:
             t = json.load(f)
     except (OSError, ValueError):
         return None, None
-    src = "profiles/traffic.json: " + t.get("source", "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs")
+    src = "profiles/traffic.json (L2 -> fabric bytes, MALL hits included): " + t.get("source", "rocprofv3 --pmc runs")
     return t.get("ag_gemm_gated_bytes_per_launch"), src
 
 
