@@ -245,10 +245,50 @@ def bench_ar(steps, warmup, producers, extra):
         ops.gemm_ar(A, B, C, peers, recv, world, flags, order, epoch=epoch[0], num_producers=producers,
                     stage_counters=counters, done_flags=done)
 
-    r = interleaved({"ar": ar, "plain": lambda i: ops.gemm(A, B, C)}, steps, warmup)
+    # Two-shot: this rank (0) reduces its own 1024-row slice from the 7
+    # peers' partials of it and receives the other 7 slices already reduced
+    # by their owners (each row reduced once across the node)
+    rank, s = 0, M // world
+    own = ops.gemm(A, B)
+    peer_src = peers[:, rank * s:(rank + 1) * s].contiguous()
+    reduced = torch.stack([(own[j * s:(j + 1) * s].float() + peers[:, j * s:(j + 1) * s].float().sum(0))
+                           .to(torch.bfloat16) for j in range(world) if j != rank])
+    del own
+    recv2 = torch.empty_like(peer_src)
+    sends = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+    nb2 = 2 * (world - 1) * s // 128
+    flags2 = torch.zeros(nb2, dtype=torch.int32, device="cuda")
+    counters2 = torch.zeros_like(flags2)
+    rbs = s // 128
+    # arrival: the partial blocks of the own slice row block by row block,
+    # then the reduced slices
+    order2_rows = torch.tensor([q * rbs + rb for rb in range(rbs) for q in range(world - 1)] +
+                               list(range((world - 1) * rbs, nb2)), dtype=torch.int32, device="cuda")
+    order2_rand = torch.from_numpy(wl.stage_order(nb2, 8)).cuda()
+    epoch2 = [0]
+
+    def ar2(order):
+        def f(i):
+            epoch2[0] += 1
+            ops.gemm_ar_two_shot(A, B, C, sends, peer_src, recv2, reduced, world, rank, flags2, order,
+                                 epoch=epoch2[0], num_producers=producers, stage_counters=counters2,
+                                 done_flags=done)
+        return f
+
+    r = interleaved({"ar": ar, "ar2_rows": ar2(order2_rows), "ar2_rand": ar2(order2_rand),
+                     "plain": lambda i: ops.gemm(A, B, C)}, steps, warmup)
     flops = 2.0 * M * N * K
     extra["gemm_ar"] = {"shape": [M, N, K], "us": r["ar"] * 1e3, "tflops": flops / r["ar"] / 1e9,
-                        "us_plain_gemm_same_shape": r["plain"] * 1e3, "staged_bytes": peers.numel() * 2}
+                        "us_plain_gemm_same_shape": r["plain"] * 1e3, "staged_bytes": peers.numel() * 2,
+                        "us_two_shot": r["ar2_rows"] * 1e3, "tflops_two_shot": flops / r["ar2_rows"] / 1e9,
+                        "us_two_shot_random_order": r["ar2_rand"] * 1e3,
+                        "two_shot_staged_bytes": (peer_src.numel() + reduced.numel()) * 2,
+                        "note": "us: one-shot, every row reduced here from the 7 staged full peer partials; "
+                                "us_two_shot: this rank reduces its 1024-row slice from the 7 peers' partials of "
+                                "it and stages the other 7 slices already reduced by their owners (the per-GPU "
+                                "work of a node-wide all-reduce that reduces each row once); partial blocks "
+                                "arrive row block by row block, then the reduced slices (random_order: a "
+                                "seeded random order over all of them)"}
 
 
 def moe_setup(cfg: wl.MoeCfg):

@@ -231,6 +231,52 @@ typedef struct mk_gemm_ar_args {
 int mk_gemm_ar(const mk_gemm_ar_args* args, void* stream);
 
 /* ------------------------------------------------------------------------ */
+/* GEMM + all-reduce at one rank's share, two-shot: this rank reduces only
+ * its own row slice and receives the other slices already reduced by their
+ * owners (reduce-scatter, then all-gather), so each output row is reduced
+ * once across the node — the work split of the reference's multicast
+ * all-reduce, where each tile is reduced once for all GPUs
+ * (reference src/gemm_ar.cu:9-32, intra-AR role with multimem reduction;
+ * include/operators/gemm_ar/session.cuh:188-215).  With s = M/world rows
+ * per slice and r = rank:
+ *   C_final[r*s .. (r+1)*s)  = bf16( (A @ B)[own rows] + sum_p peer_recv[p] )
+ *                              (fp32 adds, p ascending; the reduce epilogue)
+ *   C_final[other slices]    = peer_reduced, staged in 128-row blocks
+ *   sends[rows outside r's]  = bf16( (A @ B)[those rows] )  (this rank's pushes)
+ * One launch: flags / stage_counters / stage_order cover 2*(world-1)*s/128
+ * blocks, first the partial blocks of this rank's slice (peer_src ->
+ * peer_recv, as mk_gemm_rs), then the reduced blocks (peer_reduced ->
+ * C_final, flags[(world-1)*s/128 + b] = epoch once block b is in place).
+ * done_flags (optional, [(M/256)*(N/256)]): each finished tile of this rank's
+ * slice, as in mk_gemm_ar.  num_producers as in mk_gemm_rs; 0 = everything
+ * was staged by someone else (flags published; peer_reduced unread). */
+typedef struct mk_gemm_ar2_args {
+  const void* A;            /* bf16 [M, K] */
+  const void* B;            /* bf16 [K, N] */
+  void* C_final;            /* bf16 [M, N] */
+  void* sends;              /* bf16 [M, N]; rows outside this rank's slice written */
+  const void* peer_src;     /* bf16 [world-1, M/world, N]: peers' partials of this rank's slice, rank order without r */
+  void* peer_recv;          /* bf16 [world-1, M/world, N] staged partials */
+  const void* peer_reduced; /* bf16 [world-1, M/world, N]: the other slices, reduced, slice order without r */
+  int64_t M, N, K;
+  int32_t world, rank;
+  uint32_t* flags;              /* [2 * (world-1) * (M/world)/128] */
+  const int32_t* stage_order;   /* permutation of those blocks; NULL = ascending */
+  uint32_t epoch;
+  int32_t gated;
+  int32_t num_producers;
+  int32_t num_cus;
+  uint32_t spin_limit;
+  uint32_t* error_word;
+  uint32_t* stage_counters;     /* [2 * (world-1) * (M/world)/128] */
+  uint32_t* done_flags;         /* [(M/256) * (N/256)] or NULL */
+  void* split_ws;
+  int64_t split_ws_bytes;
+  const uint32_t* epoch_ptr;
+} mk_gemm_ar2_args;
+int mk_gemm_ar_two_shot(const mk_gemm_ar2_args* args, void* stream);
+
+/* ------------------------------------------------------------------------ */
 /* MoE routing index build (host memory, host CPU).  Restates the reference's
  * host-side builders bench/dispatch_gemm_bench.py:127-188 (build_routing,
  * build_pull_indices) and bench/dispatch_gemm_glu_combine_bench.py:222-293,

@@ -13,7 +13,7 @@ from pathlib import Path
 LIB_PATH = Path(__file__).resolve().parent / "libmk.so"
 
 ROW_BLOCK = 128
-ABI_VERSION = 6  # include/mk.h mk_abi_version(): the structures below match this layout
+ABI_VERSION = 7  # include/mk.h mk_abi_version(): the structures below match this layout
 
 EXPORTS = (
     "mk_gemm",
@@ -22,6 +22,7 @@ EXPORTS = (
     "mk_ag_gemm_noalloc_scratch_bytes",
     "mk_gemm_rs",
     "mk_gemm_ar",
+    "mk_gemm_ar_two_shot",
     "mk_moe_index_sizes",
     "mk_moe_build_indices",
     "mk_moe_index_workspace_bytes",
@@ -86,6 +87,14 @@ class GemmArArgs(C.Structure):
                 ("epoch_ptr", vp)]
 
 
+class GemmAr2Args(C.Structure):
+    _fields_ = [("A", vp), ("B", vp), ("C_final", vp), ("sends", vp), ("peer_src", vp), ("peer_recv", vp),
+                ("peer_reduced", vp), ("M", i64), ("N", i64), ("K", i64), ("world", i32), ("rank", i32),
+                ("flags", vp), ("stage_order", vp), ("epoch", u32), ("gated", i32), ("num_producers", i32),
+                ("num_cus", i32), ("spin_limit", u32), ("error_word", vp), ("stage_counters", vp),
+                ("done_flags", vp), ("split_ws", vp), ("split_ws_bytes", i64), ("epoch_ptr", vp)]
+
+
 class MoeIndex(C.Structure):
     _fields_ = [("padded_tokens_per_expert", vp), ("local_rb_per_expert", vp), ("pull_indices", vp),
                 ("row_expert", vp), ("rb_expert", vp), ("rb_rows", vp), ("row_weight", vp), ("owner_offset", vp),
@@ -138,7 +147,7 @@ def lib() -> C.CDLL:
             raise RuntimeError(f"{LIB_PATH} is missing: run __graft_entry__.build() "
                                "(or python -m mkernel_amd._build) first")
         L = C.CDLL(str(LIB_PATH))
-        for name in ("mk_gemm", "mk_ag_gemm", "mk_ag_gemm_noalloc", "mk_gemm_rs", "mk_gemm_ar", "mk_moe_permute", "mk_moe_grouped_gemm",
+        for name in ("mk_gemm", "mk_ag_gemm", "mk_ag_gemm_noalloc", "mk_gemm_rs", "mk_gemm_ar", "mk_gemm_ar_two_shot", "mk_moe_permute", "mk_moe_grouped_gemm",
                      "mk_moe_combine", "mk_moe_ffn_combine"):
             getattr(L, name).argtypes = [vp, vp]
             getattr(L, name).restype = C.c_int

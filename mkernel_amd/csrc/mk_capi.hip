@@ -222,7 +222,7 @@ extern "C" {
 
 const char* mk_last_error_string(void) { return g_err.c_str(); }
 
-int32_t mk_abi_version(void) { return 6; }
+int32_t mk_abi_version(void) { return 7; }
 
 int mk_epoch_advance(uint32_t* epoch_ptr, void* stream) {
   if (!epoch_ptr) return fail(MK_EINVAL, "mk_epoch_advance: null argument");
@@ -422,35 +422,43 @@ int mk_ag_gemm_noalloc(const mk_ag_gemm_args* a, void* stream) {
 
 int64_t mk_ag_gemm_noalloc_scratch_bytes(void) { return kNoAllocBytes; }
 
-int mk_gemm_rs(const mk_gemm_rs_args* a, void* stream) {
-  if (!a || !a->A || !a->B || !a->workspace || !a->output) return fail(MK_EINVAL, "mk_gemm_rs: null argument");
+}  // extern "C"
+
+namespace {
+// GEMM + reduce-scatter epilogue; with peer_reduced also the all-gather half
+// of a two-shot all-reduce (the other slices' reduced rows staged into
+// `output`'s full matrix, done_flags per finished own tile).  `fn` names the
+// entry point in errors.
+int rs_launch(const mk_gemm_rs_args* a, const void* peer_reduced, uint16_t* full_out, uint32_t* done_flags,
+              void* stream, const char* fn) {
+  if (!a || !a->A || !a->B || !a->workspace || !a->output) return fail(MK_EINVAL, "%s: null argument", fn);
   DevInfo d;
   if (int rc = device_info(&d)) return rc;
   const int bm = 256;
   if (int rc = check_gemm_shape(a->M, a->N, a->K, bm)) return rc;
-  if (a->world < 1 || a->rank < 0 || a->rank >= a->world) return fail(MK_EINVAL, "mk_gemm_rs: bad world/rank");
+  if (a->world < 1 || a->rank < 0 || a->rank >= a->world) return fail(MK_EINVAL, "%s: bad world/rank", fn);
   if (a->M % a->world || (a->M / a->world) % bm)
-    return fail(MK_ESHAPE, "mk_gemm_rs: M/world must be a multiple of %d", bm);
-  if (a->M / bm > mk::kMaxTilesM) return fail(MK_ESHAPE, "mk_gemm_rs: at most %d row tiles", mk::kMaxTilesM);
+    return fail(MK_ESHAPE, "%s: M/world must be a multiple of %d", fn, bm);
+  if (a->M / bm > mk::kMaxTilesM) return fail(MK_ESHAPE, "%s: at most %d row tiles", fn, mk::kMaxTilesM);
   const int npeers = a->world - 1;
-  if (npeers > 0 && !a->peer_recv) return fail(MK_EINVAL, "mk_gemm_rs: peer_recv is null");
+  if (npeers > 0 && !a->peer_recv) return fail(MK_EINVAL, "%s: peer_recv is null", fn);
   const int own_rows = (int)(a->M / a->world);
   int total;
-  if (int rc = grid_total(a->num_cus, d, "mk_gemm_rs", &total)) return rc;
-  if (a->num_producers < -6) return fail(MK_EINVAL, "mk_gemm_rs: num_producers must be >= -6");
+  if (int rc = grid_total(a->num_cus, d, fn, &total)) return rc;
+  if (a->num_producers < -6) return fail(MK_EINVAL, "%s: num_producers must be >= -6", fn);
   const bool coop = a->gated && npeers > 0 && a->num_producers < 0;
   int costage_waves = 0;
-  if (int rc = costage_request(a->gated && npeers > 0, a->num_producers, a->split_ws, a->split_ws_bytes, stream,
-                               "mk_gemm_rs", &costage_waves))
+  if (int rc = costage_request(a->gated && npeers > 0, a->num_producers, a->split_ws, a->split_ws_bytes, stream, fn,
+                               &costage_waves))
     return rc;
   const int n_prod = (a->gated && npeers > 0 && a->num_producers > 0) ? a->num_producers : 0;
   if (a->gated && npeers > 0) {
-    if (!a->flags) return fail(MK_EINVAL, "mk_gemm_rs: gated launch needs flags");
-    if (a->epoch == 0 && !a->epoch_ptr) return fail(MK_EINVAL, "mk_gemm_rs: epoch 0 is reserved");
-    if (a->num_producers != 0 && !a->peer_src) return fail(MK_EINVAL, "mk_gemm_rs: staging needs peer_src");
-    if (coop && !a->stage_counters) return fail(MK_EINVAL, "mk_gemm_rs: cooperative staging needs stage_counters");
+    if (!a->flags) return fail(MK_EINVAL, "%s: gated launch needs flags", fn);
+    if (a->epoch == 0 && !a->epoch_ptr) return fail(MK_EINVAL, "%s: epoch 0 is reserved", fn);
+    if (a->num_producers != 0 && !a->peer_src) return fail(MK_EINVAL, "%s: staging needs peer_src", fn);
+    if (coop && !a->stage_counters) return fail(MK_EINVAL, "%s: cooperative staging needs stage_counters", fn);
   }
-  if (n_prod >= total) return fail(MK_EINVAL, "mk_gemm_rs: bad num_producers");
+  if (n_prod >= total) return fail(MK_EINVAL, "%s: bad num_producers", fn);
   mk::GemmKParams p;
   fill_common(p);
   p.A = static_cast<const uint16_t*>(a->A);
@@ -469,6 +477,7 @@ int mk_gemm_rs(const mk_gemm_rs_args* a, void* stream) {
   p.rs_npeers = npeers;
   p.rs_recv = static_cast<const uint16_t*>(a->peer_recv);
   p.rs_out = static_cast<uint16_t*>(a->output);
+  p.ar_done = done_flags;
   p.epoch = a->epoch;
   p.epoch_ptr = a->epoch_ptr;
   p.spin_limit = a->spin_limit;
@@ -480,6 +489,16 @@ int mk_gemm_rs(const mk_gemm_rs_args* a, void* stream) {
       p.st_dst = static_cast<uint16_t*>(a->peer_recv);
       p.st_cols = (int)a->N;
       p.st_nblocks = npeers * (own_rows / 128);
+      if (peer_reduced) {
+        // all-gather half: the peers' reduced slices, in slice order
+        // without this rank's, into full_out around this rank's slice
+        p.st_src2 = static_cast<const uint16_t*>(peer_reduced);
+        p.st_dst2 = full_out;
+        p.st_split_at = p.st_nblocks;
+        p.st_dst2_skip_at = a->rank * (own_rows / 128);
+        p.st_dst2_skip = own_rows / 128;
+        p.st_nblocks *= 2;
+      }
       p.st_order = a->stage_order;
       p.st_flags = a->flags;
       p.st_counters = a->stage_counters;
@@ -490,12 +509,43 @@ int mk_gemm_rs(const mk_gemm_rs_args* a, void* stream) {
         p.st_claim = reinterpret_cast<uint32_t*>(static_cast<char*>(a->split_ws) + kClaimOffset);
     }
   }
-  if (int rc = check_ws(a->split_ws, a->split_ws_bytes, "mk_gemm_rs")) return rc;
+  if (int rc = check_ws(a->split_ws, a->split_ws_bytes, fn)) return rc;
   plan_split(p, bm, a->split_ws, a->split_ws_bytes);
   hipError_t e = costage_waves ? mk::launch_gemm_costaged(p, mk::kEpiReduce, costage_waves * total,
                                                           static_cast<hipStream_t>(stream))
                                : mk::launch_gemm(p, bm, mk::kEpiReduce, static_cast<hipStream_t>(stream));
-  return e == hipSuccess ? MK_OK : hip_fail(e, "mk_gemm_rs launch");
+  return e == hipSuccess ? MK_OK : hip_fail(e, fn);
+}
+}  // namespace
+
+extern "C" {
+
+int mk_gemm_rs(const mk_gemm_rs_args* a, void* stream) {
+  return rs_launch(a, nullptr, nullptr, nullptr, stream, "mk_gemm_rs");
+}
+
+int mk_gemm_ar_two_shot(const mk_gemm_ar2_args* a, void* stream) {
+  if (!a || !a->C_final) return fail(MK_EINVAL, "mk_gemm_ar_two_shot: null argument");
+  if (a->world < 1 || a->rank < 0 || a->rank >= a->world || a->M % a->world)
+    return fail(MK_EINVAL, "mk_gemm_ar_two_shot: bad world/rank");
+  const bool staging = a->gated && a->world > 1 && a->num_producers != 0;
+  if (staging && !a->peer_reduced) return fail(MK_EINVAL, "mk_gemm_ar_two_shot: staging needs peer_reduced");
+  if (a->done_flags && a->epoch == 0 && !a->epoch_ptr)
+    return fail(MK_EINVAL, "mk_gemm_ar_two_shot: epoch 0 is reserved");
+  mk_gemm_rs_args r;
+  std::memset(&r, 0, sizeof r);
+  r.A = a->A; r.B = a->B;
+  r.workspace = a->sends;
+  r.output = static_cast<uint16_t*>(a->C_final) + (int64_t)a->rank * (a->M / a->world) * a->N;
+  r.peer_src = a->peer_src; r.peer_recv = a->peer_recv;
+  r.M = a->M; r.N = a->N; r.K = a->K;
+  r.world = a->world; r.rank = a->rank;
+  r.flags = a->flags; r.stage_order = a->stage_order; r.epoch = a->epoch; r.gated = a->gated;
+  r.num_producers = a->num_producers; r.num_cus = a->num_cus; r.spin_limit = a->spin_limit;
+  r.error_word = a->error_word; r.stage_counters = a->stage_counters;
+  r.split_ws = a->split_ws; r.split_ws_bytes = a->split_ws_bytes; r.epoch_ptr = a->epoch_ptr;
+  return rs_launch(&r, staging ? a->peer_reduced : nullptr, static_cast<uint16_t*>(a->C_final), a->done_flags,
+                   stream, "mk_gemm_ar_two_shot");
 }
 
 int mk_gemm_ar(const mk_gemm_ar_args* a, void* stream) {

@@ -132,13 +132,28 @@ __device__ __forceinline__ uint32_t launch_epoch(const GemmKParams& p) {
 // ---------------------------------------------------------------------------
 // Producer role: copy 128-row blocks src -> dst in stage order, then publish.
 // ---------------------------------------------------------------------------
+// Source and destination of staged block b (see st_split_at).
+__device__ __forceinline__ void stage_block(const GemmKParams& p, int b, const uint16_t*& src, uint16_t*& dst) {
+  const int64_t block_elems = (int64_t)kFlagRows * p.st_cols;
+  if (p.st_src2 && b >= p.st_split_at) {
+    const int b2 = b - p.st_split_at;
+    src = p.st_src2 + (int64_t)b2 * block_elems;
+    dst = p.st_dst2 + (int64_t)(b2 + (b2 >= p.st_dst2_skip_at ? p.st_dst2_skip : 0)) * block_elems;
+  } else {
+    src = p.st_src + (int64_t)b * block_elems;
+    dst = p.st_dst + (int64_t)b * block_elems;
+  }
+}
+
 template <int NT>
 __device__ void producer_role(const GemmKParams& p, int pid) {
   const int64_t block_elems = (int64_t)kFlagRows * p.st_cols;
   for (int i = pid; i < p.st_nblocks; i += p.n_prod) {
     const int b = p.st_order ? p.st_order[i] : i;
-    if (i >= p.st_present)
-      copy_wt<NT, 16>(p.st_src + (int64_t)b * block_elems, p.st_dst + (int64_t)b * block_elems, block_elems / 8);
+    const uint16_t* src;
+    uint16_t* dst;
+    stage_block(p, b, src, dst);
+    if (i >= p.st_present) copy_wt<NT, 16>(src, dst, block_elems / 8);
     // every wave's write-through stores performed, then one publication
     wait_vmem_all();
     __syncthreads();
@@ -157,8 +172,11 @@ __device__ __forceinline__ int stage_piece(const GemmKParams& p, int q) {
   const int64_t piece_vec = block_elems / 8 / kPieces;  // 16-byte units per piece
   const int pos = q / kPieces, piece = q % kPieces;
   const int b = p.st_order ? p.st_order[pos] : pos;
-  const int64_t off = (int64_t)b * block_elems + (int64_t)piece * piece_vec * 8;
-  if (pos >= p.st_present) copy_wt<NT, U>(p.st_src + off, p.st_dst + off, piece_vec);
+  const uint16_t* src;
+  uint16_t* dst;
+  stage_block(p, b, src, dst);
+  const int64_t off = (int64_t)piece * piece_vec * 8;
+  if (pos >= p.st_present) copy_wt<NT, U>(src + off, dst + off, piece_vec);
   return b;
 }
 

@@ -57,6 +57,14 @@ struct GemmKParams {
   const uint16_t* st_src;
   uint16_t* st_dst;
   int st_cols, st_nblocks;
+  // Blocks at index >= st_split_at (when st_src2 is set) form a second
+  // staging set: block st_split_at + b copies st_src2 block b to st_dst2
+  // block b, or b + st_dst2_skip from block st_dst2_skip_at on (the
+  // all-gather half of a two-shot all-reduce: the other slices' reduced
+  // rows into C_final, around this rank's own slice).
+  const uint16_t* st_src2;
+  uint16_t* st_dst2;
+  int st_split_at, st_dst2_skip_at, st_dst2_skip;
   int st_present;           // stage positions < st_present hold blocks already in st_dst: published, not copied
   const int* st_order;
   uint32_t* st_flags;

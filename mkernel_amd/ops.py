@@ -12,7 +12,7 @@ import numpy as np
 import torch
 
 from . import capi
-from .capi import (AgGemmArgs, GemmArArgs, GemmArgs, GemmRsArgs, MoeCombineArgs, MoeFfnArgs, MoeGroupedGemmArgs,
+from .capi import (AgGemmArgs, GemmAr2Args, GemmArArgs, GemmArgs, GemmRsArgs, MoeCombineArgs, MoeFfnArgs, MoeGroupedGemmArgs,
                    MoeIndex, MoeIndexDevArgs, MoePermuteArgs)
 
 
@@ -147,6 +147,28 @@ def gemm_ar(A, B, C_final, peer_src, peer_recv, world: int, flags, stage_order, 
                       _ptr(stage_order), epoch, int(gated), num_producers, num_cus, spin_limit, _ptr(error_word),
                       _ptr(stage_counters), _ptr(done_flags), *_ws(split_ws, A.device), _ptr(epoch_ptr))
     capi.call("mk_gemm_ar", args, _stream())
+    return C_final
+
+
+def gemm_ar_two_shot(A, B, C_final, sends, peer_src, peer_recv, peer_reduced, world: int, rank: int, flags,
+                     stage_order, epoch: int, gated: bool = True, num_producers: int = -1, num_cus: int = 0,
+                     spin_limit: int = 0, error_word=None, stage_counters=None, done_flags=None, split_ws=None,
+                     epoch_ptr=None) -> torch.Tensor:
+    """GEMM + all-reduce at one rank's share, two-shot (mk_gemm_ar_two_shot):
+    this rank's slice of C_final = A @ B + the world-1 staged peer partials
+    of that slice ([world-1, M/world, N]); the other slices are the peers'
+    reduced rows ``peer_reduced`` ([world-1, M/world, N], slice order
+    without ``rank``), staged in; ``sends`` gets this rank's partial rows of
+    the other slices.  flags / stage_counters / stage_order cover
+    2*(world-1)*(M/world)/128 blocks (partials first, then reduced rows)."""
+    _bf16(A, "A"); _bf16(B, "B"); _bf16(C_final, "C_final"); _bf16(sends, "sends")
+    M, K = A.shape
+    N = B.shape[1]
+    args = GemmAr2Args(_ptr(A), _ptr(B), _ptr(C_final), _ptr(sends), _ptr(peer_src), _ptr(peer_recv),
+                       _ptr(peer_reduced), M, N, K, world, rank, _ptr(flags), _ptr(stage_order), epoch, int(gated),
+                       num_producers, num_cus, spin_limit, _ptr(error_word), _ptr(stage_counters), _ptr(done_flags),
+                       *_ws(split_ws, A.device), _ptr(epoch_ptr))
+    capi.call("mk_gemm_ar_two_shot", args, _stream())
     return C_final
 
 

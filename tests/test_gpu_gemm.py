@@ -354,6 +354,65 @@ def test_gemm_ar_vs_oracle(dev, producers, num_cus, M, N, K):
     assert torch.equal(outs[0], outs[1]), "result depends on the stage order"
 
 
+@pytest.mark.parametrize("world,rank,producers,num_cus", [(8, 3, -1, 0), (8, 0, 4, 0), (4, 2, -3, 0), (8, 7, 0, 0),
+                                                        (2, 1, -1, 8), (8, 5, -1, 3)])
+def test_gemm_ar_two_shot_vs_oracle(dev, world, rank, producers, num_cus):
+    """Two-shot all-reduce at one rank's share: the rank's own slice is
+    A@B + the world-1 peer partials of that slice (fp32 adds, oracle
+    tolerance), every other slice is the peers' reduced rows copied in bit
+    for bit, the sends hold this rank's partial rows of the other slices,
+    every staged block's flag and every own tile's done flag carry the
+    epoch.  producers 0: everything staged before the launch."""
+    _say(f"gemm_ar two-shot world={world} rank={rank} producers={producers} num_cus={num_cus}")
+    M, N, K = 512 * world // 2 if world > 2 else 1024, 512, 256
+    s = M // world
+    A = wl.randn_bf16((M, K), 70, K ** -0.5)
+    B = wl.randn_bf16((K, N), 71, K ** -0.5)
+    P = wl.randn_bf16((world - 1, M, N), 72, 0.5)  # the peers' full partials, rank order without `rank`
+    own = gemm_ref(A, B)
+    others = [j for j in range(world) if j != rank]
+    peer_src = P[:, rank * s:(rank + 1) * s].contiguous()
+    reduced = torch.stack([(own[j * s:(j + 1) * s] + P[:, j * s:(j + 1) * s].float().sum(0)).to(torch.bfloat16)
+                           for j in others])
+    ref_own = own[rank * s:(rank + 1) * s].clone()
+    for q in range(world - 1):
+        ref_own += peer_src[q].float()
+    nb = 2 * (world - 1) * s // 128
+    C_final = torch.zeros((M, N), dtype=torch.bfloat16, device=dev)
+    sends = torch.zeros((M, N), dtype=torch.bfloat16, device=dev)
+    done = torch.zeros((M // 256) * (N // 256), dtype=torch.int32, device=dev)
+    counters = torch.zeros(nb, dtype=torch.int32, device=dev)
+    err = torch.zeros(1, dtype=torch.int32, device=dev)
+    order = torch.from_numpy(wl.stage_order(nb, 13)).to(dev)
+    if producers == 0:
+        recv = peer_src.to(dev)
+        for i, j in enumerate(others):
+            C_final[j * s:(j + 1) * s] = reduced[i].to(dev)
+        flags = torch.full((nb,), 4, dtype=torch.int32, device=dev)
+    else:
+        recv = torch.zeros_like(peer_src, device=dev)
+        flags = torch.zeros(nb, dtype=torch.int32, device=dev)
+    ops.gemm_ar_two_shot(A.to(dev), B.to(dev), C_final, sends, peer_src.to(dev), recv, reduced.to(dev), world, rank,
+                         flags, order, epoch=4, num_producers=producers, num_cus=num_cus, stage_counters=counters,
+                         done_flags=done, spin_limit=4_000_000, error_word=err)
+    torch.cuda.synchronize()
+    assert int(err.item()) == 0
+    Cf = C_final.cpu()
+    assert rel_fro(Cf[rank * s:(rank + 1) * s].float(), ref_own) < TOL
+    for i, j in enumerate(others):
+        assert torch.equal(Cf[j * s:(j + 1) * s], reduced[i]), f"slice {j} not copied exactly"
+    mask = torch.ones(M, dtype=torch.bool)
+    mask[rank * s:(rank + 1) * s] = False
+    assert rel_fro(sends.cpu()[mask].float(), own[mask]) < TOL
+    assert (sends.cpu()[~mask] == 0).all()
+    assert (flags.cpu() == 4).all()
+    tiles_n = N // 256
+    own_tiles = [t for t in range(done.numel()) if rank * s <= (t // tiles_n) * 256 < (rank + 1) * s]
+    assert (done.cpu()[own_tiles] == 4).all()
+    if producers:
+        assert torch.equal(recv.cpu(), peer_src)
+
+
 def test_gemm_ar_equal_partials_known_answer(dev):
     """Every peer partial equal to the own partial => C_final is exactly 8x
     it (integer operands, exact in fp32 and bf16)."""
