@@ -28,10 +28,10 @@ def test_library_exports_every_declared_symbol():
     L = capi.lib()
     for name in _header_symbols():
         assert hasattr(L, name), name
-    assert L.mk_abi_version() == capi.ABI_VERSION == 6
+    assert L.mk_abi_version() == capi.ABI_VERSION == 7
 
 
-_STRUCTS = {"mk_gemm_args": capi.GemmArgs, "mk_gemm_ar_args": capi.GemmArArgs, "mk_ag_gemm_args": capi.AgGemmArgs, "mk_gemm_rs_args": capi.GemmRsArgs,
+_STRUCTS = {"mk_gemm_args": capi.GemmArgs, "mk_gemm_ar_args": capi.GemmArArgs, "mk_gemm_ar2_args": capi.GemmAr2Args, "mk_ag_gemm_args": capi.AgGemmArgs, "mk_gemm_rs_args": capi.GemmRsArgs,
             "mk_moe_index": capi.MoeIndex, "mk_moe_permute_args": capi.MoePermuteArgs,
             "mk_moe_grouped_gemm_args": capi.MoeGroupedGemmArgs, "mk_moe_combine_args": capi.MoeCombineArgs,
             "mk_moe_ffn_args": capi.MoeFfnArgs, "mk_moe_index_dev_args": capi.MoeIndexDevArgs}
