@@ -136,9 +136,11 @@ int mk_ag_gemm(const mk_ag_gemm_args* args, void* stream);
  * 32 MB, one copy per GPU, held until the process ends); split_ws,
  * split_ws_bytes and stage_counters must be NULL / 0.  Limits: M/128 <=
  * 16384 row blocks (larger M returns MK_ESHAPE); a tail round whose K-split
- * would need more than 128 partial tiles runs unsplit.  Each call first
- * clears the counters and split flags it uses on `stream` (a small kernel),
- * then launches mk_ag_gemm's kernels.  Every call on one GPU shares that
+ * would need more than 128 partial tiles runs unsplit; num_producers <= -3
+ * (the co-resident staging kernel, whose side stream and events the library
+ * creates on first use) stages cooperatively (-1) instead.  Each call checks
+ * every argument, then clears the counters, split flags and claim words it
+ * uses on `stream` (a small kernel), then launches mk_ag_gemm's kernels.  Every call on one GPU shares that
  * GPU's array: calls that overlap in time on one GPU (different streams)
  * race and must not be issued. */
 int mk_ag_gemm_noalloc(const mk_ag_gemm_args* args, void* stream);
