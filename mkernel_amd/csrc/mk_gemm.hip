@@ -730,13 +730,28 @@ __device__ __forceinline__ void add_partial_regs(const float* src, f32x16 (&acc)
 // Compute role
 //
 // Work of one consumer: the tiles cons_id, cons_id + n_cons, ... below
-// sk_full (whole K each), then, when the tile count leaves a partial last
+// sk_full (whole K each; a partial last round of whole tiles goes to
+// consumers spread over the XCDs, xcd_slot), then, when the tile count leaves a partial last
 // round (sk_split > 1), one K-split unit of a tail tile: consumer u works on
 // tail tile sk_full + u / sk_split, K part u % sk_split.  Parts 1.. write
 // fp32 partials to the workspace and release a flag; part 0 acquires the
 // flags, adds the partials in part order (deterministic) and runs the
 // epilogue.  Every round then keeps all consumers busy.
 // ---------------------------------------------------------------------------
+// Slot of consumer c among `count` < n_cons slots of a partial round,
+// spread evenly over the 8 XCDs (consumer c sits on XCD c / (n_cons / 8)
+// after the XCD remap), or -1 when c has none.  Leaving every XCD a few
+// idle CUs instead of leaving whole XCDs idle measured faster: an
+// 8192x3584x8192 GEMM (448 tiles: one full round + 192 tiles) took 364 us
+// against 400 us with the idle CUs on two XCDs (the loaded XCDs clock
+// lower).  Which tile a workgroup computes does not change any output bit.
+__device__ __forceinline__ int xcd_slot(int c, int n_cons, int count, bool spread) {
+  if (!spread || (n_cons & 7) || count >= n_cons) return c < count ? c : -1;
+  const int per = n_cons / 8, x = c / per, j = c % per, base = count / 8, rem = count % 8;
+  if (j >= base + (x < rem ? 1 : 0)) return -1;
+  return x * base + min(x, rem) + j;
+}
+
 template <class C, int EPI>
 __device__ __forceinline__ void compute_role(const GemmKParams& p, int cons_id, int n_cons, char* smem,
                                              const int* row_perm, const uint16_t* full_list, StagePlan& sp) {
@@ -795,7 +810,13 @@ __device__ __forceinline__ void compute_role(const GemmKParams& p, int cons_id, 
 
   const int full = (sk_split > 1) ? sk_full : ntiles;
   const int n_tail_units = (ntiles - full) * (sk_split > 1 ? sk_split : 0);
-  const int n_full_mine = (full > cons_id) ? (full - cons_id + n_cons - 1) / n_cons : 0;
+  // Whole tiles: rounds 0 .. last_round-1 complete, then a partial round of
+  // last_cnt tiles spread over the XCDs.  (The K-split tail units stay in
+  // consumer order: spreading them split the grouped order's 8-row-tile
+  // runs across XCDs and measured slower on the MoE GEMM1.)
+  const int last_cnt = full % n_cons, last_round = full / n_cons;
+  const int last_slot = xcd_slot(cons_id, n_cons, last_cnt, p.xcd_remap != 0);
+  const int n_full_mine = last_round + (last_slot >= 0 ? 1 : 0);
 
   // One output tile (or one K range of it): accumulate A[rows] @ B[:, cols]
   // over K stages k0 .. k0+nk into acc.  Called from two places (whole
@@ -1164,7 +1185,7 @@ __device__ __forceinline__ void compute_role(const GemmKParams& p, int cons_id, 
       const int even = (int)((int64_t)st_total * (w + 1) / sp.n_rounds);
       coop_stage<C::NT>(p, n_cons, sp.q, sp.batch, max(need, even));
     }
-    int t = cons_id + w * n_cons;
+    int t = (w < last_round ? cons_id : last_slot) + w * n_cons;
     if (full_list) t = full_list[t];
     f32x16 acc[C::FM][C::FN];
     int m0, tn;

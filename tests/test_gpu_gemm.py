@@ -77,6 +77,29 @@ def test_gemm_split_tail(dev, M, N, K, tile, cus):
     assert int(ws[:4096].view(torch.int32).abs().sum()) == 0, "split flags not left zeroed"
 
 
+@pytest.mark.parametrize("M,N,K,cus", [(8192, 3584, 256, 0),    # 448 tiles: one round + 192 spread over the XCDs
+                                       (4096, 3584, 512, 0),    # 224 tiles: one partial round
+                                       (4096, 3584, 256, 128),  # 224 on 128: one round + 96
+                                       (4096, 3584, 256, 130)])  # grid not a multiple of 8: consumer order
+def test_gemm_partial_round_every_tile(dev, M, N, K, cus):
+    """A partial last round of whole tiles (too many tiles to K-split) is
+    dealt to consumers spread over the XCDs: every tile is written once and
+    matches the oracle, and the result is bit-equal across grids."""
+    _say(f"gemm partial round M={M} N={N} K={K} cus={cus}")
+    A = wl.randn_bf16((M, K), 23, K ** -0.5)
+    B = wl.randn_bf16((K, N), 24, K ** -0.5)
+    C = torch.full((M, N), float("nan"), dtype=torch.bfloat16, device=dev)
+    ops.gemm(A.to(dev), B.to(dev), C, num_cus=cus, tile_m=256)
+    torch.cuda.synchronize()
+    ref = gemm_ref(A, B)
+    assert not torch.isnan(C).any(), "a tile of the partial round was not written"
+    assert torch.allclose(C.cpu().float(), ref, rtol=2 ** -7, atol=1e-5)
+    # 256-row tiles, no K-split on these shapes: every element is one fp32
+    # dot product in K order, so any grid gives the same bits
+    C8 = ops.gemm(A.to(dev), B.to(dev), num_cus=8, tile_m=256)
+    assert torch.equal(C, C8)
+
+
 def test_gemm_split_identity_exact(dev):
     """With a 4-way K split, I @ X is still exact (partials are exact sums)."""
     n = 1024
