@@ -46,7 +46,8 @@ typedef struct mk_gemm_args {
   int64_t M, N, K;
   int64_t lda, ldb, ldc;
   int32_t num_cus; /* persistent grid size; 0 = every CU of the device; at most the CU count */
-  int32_t tile_m;  /* 0 = auto, else 128 or 256 */
+  int32_t tile_m;  /* 0 = auto (256 unless 128-row tiles fit in one round
+                      of the grid), else 128 or 256 */
   int32_t waves;   /* waves per workgroup: 0 = auto, 4 (one per SIMD) or 8 (two per SIMD) */
   void* split_ws;          /* optional K-split workspace (see mk_query_workspace_bytes);
                               zero-filled before its first use, left zeroed by every
