@@ -121,6 +121,8 @@ def bench_ag(steps, warmup, producers, extra):
         # gated, flags already published (pure gating cost, all CUs computing)
         "preset": lambda i: ops.ag_gemm(None, A_full, B, C, flags_pub, order_d, epoch=2 ** 30, num_producers=0),
         "own_shard_local": gated_own,
+        # the vendor library (torch.matmul = hipBLASLt) on the same operands
+        "torch_matmul": lambda i: torch.matmul(A_full, B, out=C),
     }, steps, warmup)
     ms_med, ms_dedicated, ms_ungated, ms_preset = r["gated"], r["dedicated"], r["ungated"], r["preset"]
     # the headline: W warmup steps, then exactly K timed steps of the gated
@@ -134,6 +136,7 @@ def bench_ag(steps, warmup, producers, extra):
         "us_gated_32_dedicated_producers": ms_dedicated * 1e3,
         "us_gated_even_share_staging": r["even_share"] * 1e3,
         "us_gated_coresident_staging_kernel": r["coresident"] * 1e3,
+        "us_torch_matmul_ungated": r["torch_matmul"] * 1e3,
         "tflops_gated_producer": flops / ms / 1e9, "tflops_ungated": flops / ms_ungated / 1e9,
         "gating_overhead_producer": ms_med / ms_ungated - 1.0,
         "gating_overhead_flag_check": ms_preset / ms_ungated - 1.0,
@@ -157,8 +160,12 @@ def bench_gemm(steps, warmup, extra):
     # average excludes the empty-queue start (one host launch latency) that
     # a synchronize-bracketed region of a ~0.1 ms kernel includes
     ms_primed = Timer().run(lambda i: ops.gemm(A, B, C), max(steps, 50), max(warmup, 5), primed=True)
+    # the vendor library on the same data in the same process, interleaved
+    # (torch.matmul is hipBLASLt here): a same-box comparison
+    rv = interleaved({"mk": lambda i: ops.gemm(A, B, C), "torch": lambda i: torch.matmul(A, B, out=C)}, steps, warmup)
     extra["gemm_4096"] = {"us": ms * 1e3, "tflops": flops / ms / 1e9, "frac_peak": flops / ms / 1e9 / PEAK_BF16_TFLOPS,
-                          "us_back_to_back": ms_primed * 1e3, "tflops_back_to_back": flops / ms_primed / 1e9}
+                          "us_back_to_back": ms_primed * 1e3, "tflops_back_to_back": flops / ms_primed / 1e9,
+                          "us_interleaved": rv["mk"] * 1e3, "us_torch_matmul_interleaved": rv["torch"] * 1e3}
 
 
 def bench_rs(steps, warmup, producers, extra):
