@@ -109,28 +109,56 @@ __device__ int block_exclusive_scan(int v, int* s, int& total) {
 }
 
 constexpr int kPlanThreads = 1024;
+constexpr int kPlanSteps = 4;  // chunk counts of one expert loaded together: 64 x kPlanSteps per wave
+constexpr int kTokSeg = 8;     // token counts per thread in one block scan (kPlanThreads x kTokSeg tokens)
 
+// One workgroup; a chain of dependent steps, so every step issues its loads
+// together: the first token segment is loaded at kernel start (the token
+// scan does not depend on the expert work), each wave loads up to
+// 64 x kPlanSteps chunk counts of an expert before scanning them, and the
+// per-expert totals go through LDS as well as global memory.
 __global__ __launch_bounds__(kPlanThreads) void plan_kernel(IndexKParams p) {
   __shared__ int s[kPlanThreads];
+  __shared__ int cnt_s[kPlanThreads];  // exp_cnt of experts below kPlanThreads
   __shared__ int carry;
-  // per expert: totals, and the exclusive prefix over chunks (in place);
-  // one wave per expert, 64 chunks per step, wave prefix sums by shuffles
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  // token pass 0: tokens t0 .. t0 + n, thread i holding `per` consecutive ones
+  const int n0 = min(p.T, kPlanThreads * kTokSeg);
+  const int per0 = (n0 + kPlanThreads - 1) / kPlanThreads;
+  int tv[kTokSeg];
+#pragma unroll
+  for (int k = 0; k < kTokSeg; ++k) {
+    const int t = threadIdx.x * per0 + k;
+    tv[k] = (k < per0 && t < n0) ? p.tok[t] : 0;
+  }
+  // per expert: totals, and the exclusive prefix over chunks (in place);
+  // one wave per expert, wave prefix sums by shuffles
   for (int e = wave; e < p.n_local; e += kPlanThreads / 64) {
     int* h = p.hist + (int64_t)e * p.nchunks;
     int carry_e = 0;
-    for (int c0 = 0; c0 < p.nchunks; c0 += 64) {
-      const int c = c0 + lane;
-      const int v = c < p.nchunks ? h[c] : 0;
-      int incl = v;
-      for (int d = 1; d < 64; d <<= 1) {
-        const int y = __shfl_up(incl, d, 64);
-        if (lane >= d) incl += y;
+    for (int c0 = 0; c0 < p.nchunks; c0 += 64 * kPlanSteps) {
+      int v[kPlanSteps];
+#pragma unroll
+      for (int k = 0; k < kPlanSteps; ++k) {
+        const int c = c0 + 64 * k + lane;
+        v[k] = c < p.nchunks ? h[c] : 0;
       }
-      if (c < p.nchunks) h[c] = carry_e + incl - v;
-      carry_e += __shfl(incl, 63, 64);
+#pragma unroll
+      for (int k = 0; k < kPlanSteps; ++k) {
+        const int c = c0 + 64 * k + lane;
+        int incl = v[k];
+        for (int d = 1; d < 64; d <<= 1) {
+          const int y = __shfl_up(incl, d, 64);
+          if (lane >= d) incl += y;
+        }
+        if (c < p.nchunks) h[c] = carry_e + incl - v[k];
+        carry_e += __shfl(incl, 63, 64);
+      }
     }
-    if (lane == 0) p.exp_cnt[e] = carry_e;
+    if (lane == 0) {
+      p.exp_cnt[e] = carry_e;
+      if (e < kPlanThreads) cnt_s[e] = carry_e;
+    }
   }
   __syncthreads();
   // padded expert offsets: exclusive scan over experts, kPlanThreads at a time
@@ -139,12 +167,13 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(IndexKParams p) {
   int64_t routed = 0;
   for (int e0 = 0; e0 < p.n_local; e0 += kPlanThreads) {
     const int e = e0 + threadIdx.x;
-    const int cnt = e < p.n_local ? p.exp_cnt[e] : 0;
+    const int cnt = e < p.n_local ? (e < kPlanThreads ? cnt_s[e] : p.exp_cnt[e]) : 0;
     const int padded = (cnt + p.row_block - 1) / p.row_block * p.row_block;
     int tot;
     const int ex = block_exclusive_scan<kPlanThreads>(padded, s, tot);
     if (e < p.n_local) {
       p.exp_off[e] = carry + ex;
+      if (e < kPlanThreads) cnt_s[e] = carry + ex;  // now the expert's row offset
       if (p.out.padded_tokens_per_expert) p.out.padded_tokens_per_expert[e] = padded;
       if (p.out.local_rb_per_expert) p.out.local_rb_per_expert[e] = cnt / p.row_block;
     }
@@ -164,18 +193,34 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(IndexKParams p) {
   // chunk prefixes become absolute row bases
   for (int e = wave; e < p.n_local; e += kPlanThreads / 64) {
     int* h = p.hist + (int64_t)e * p.nchunks;
-    const int off = p.exp_off[e];
+    const int off = e < kPlanThreads ? cnt_s[e] : p.exp_off[e];
     for (int c = lane; c < p.nchunks; c += 64) h[c] += off;
   }
   // token CSR offsets: exclusive prefix of the per-token counts (the
-  // offsets pass, merged into the same launch)
+  // offsets pass, merged into the same launch), kPlanThreads x kTokSeg
+  // tokens per block scan
   int tcarry = 0;
-  for (int t0 = 0; t0 < p.T; t0 += kPlanThreads) {
-    const int t = t0 + threadIdx.x;
-    const int v = t < p.T ? p.tok[t] : 0;
+  for (int t0 = 0; t0 < p.T; t0 += kPlanThreads * kTokSeg) {
+    const int n = min(p.T - t0, kPlanThreads * kTokSeg);
+    const int per = (n + kPlanThreads - 1) / kPlanThreads;
+    const int tb = t0 + threadIdx.x * per;
+    int v[kTokSeg], sum = 0;
+#pragma unroll
+    for (int k = 0; k < kTokSeg; ++k) {
+      v[k] = t0 == 0 ? tv[k] : ((k < per && tb + k < t0 + n) ? p.tok[tb + k] : 0);
+      sum += v[k];
+    }
     int tot;
-    const int ex = block_exclusive_scan<kPlanThreads>(v, s, tot);
-    if (t < p.T && p.out.owner_offset) p.out.owner_offset[t] = tcarry + ex;
+    const int ex = block_exclusive_scan<kPlanThreads>(sum, s, tot);
+    if (p.out.owner_offset) {
+      int run = tcarry + ex;
+#pragma unroll
+      for (int k = 0; k < kTokSeg; ++k)
+        if (k < per && tb + k < t0 + n) {
+          p.out.owner_offset[tb + k] = run;
+          run += v[k];
+        }
+    }
     tcarry += tot;
   }
   if (threadIdx.x == 0 && p.out.owner_offset) p.out.owner_offset[p.T] = tcarry;
