@@ -100,6 +100,31 @@ def test_gemm_partial_round_every_tile(dev, M, N, K, cus):
     assert torch.equal(C, C8)
 
 
+def test_gemm_random_shapes_and_grids(dev):
+    """Seeded random shapes, grid sizes and tile heights: whatever mix of
+    whole rounds, spread partial rounds and K-split tails the planner picks,
+    every output matches the oracle (one fp32 dot product per element up to
+    the split's fp32 rounding) and no tile is left unwritten."""
+    rng = np.random.default_rng(2024)
+    cus = ops.cu_count()
+    for case in range(16):
+        M = int(rng.integers(1, 17)) * 256
+        N = int(rng.integers(1, 13)) * 256
+        K = int(rng.integers(1, 33)) * 32
+        grid = int(rng.choice([0, 0, 8, 24, 64, 96, 130, 200, cus]))
+        tile = int(rng.choice([0, 128, 256]))
+        _say(f"gemm random case={case} M={M} N={N} K={K} grid={grid} tile={tile}")
+        A = wl.randn_bf16((M, K), 100 + case, K ** -0.5)
+        B = wl.randn_bf16((K, N), 200 + case, K ** -0.5)
+        C = torch.full((M, N), float("nan"), dtype=torch.bfloat16, device=dev)
+        ops.gemm(A.to(dev), B.to(dev), C, num_cus=grid, tile_m=tile)
+        torch.cuda.synchronize()
+        assert not torch.isnan(C).any(), f"case {case}: unwritten tiles"
+        ref = gemm_ref(A, B)
+        assert rel_fro(C.float(), ref) < TOL, f"case {case}"
+        assert torch.allclose(C.cpu().float(), ref, rtol=2 ** -6, atol=1e-4), f"case {case}"
+
+
 def test_gemm_split_identity_exact(dev):
     """With a 4-way K split, I @ X is still exact (partials are exact sums)."""
     n = 1024
