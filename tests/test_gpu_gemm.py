@@ -185,6 +185,41 @@ def test_ag_gemm_producer_gated(dev, producers):
         assert int(ws[4096 - 64:4096].cpu().count_nonzero()) == 0
 
 
+def test_ag_gemm_random_shapes_and_grids(dev):
+    """Seeded random AllGather shapes, grids and producer modes: the staged
+    A_full is a bit-exact copy, every flag is published, and the gated
+    result is bit-equal to the ungated GEMM on the same grid (same K-split
+    plan), whatever rounds, spread partial rounds and tails the plan has."""
+    rng = np.random.default_rng(77)
+    for case in range(10):
+        world = int(rng.choice([2, 4, 8]))
+        shard = int(rng.integers(1, 9)) * 256
+        N = int(rng.integers(1, 15)) * 256
+        K = int(rng.integers(1, 17)) * 64
+        grid = int(rng.choice([0, 0, 16, 64, 128, 200]))
+        prod = int(rng.choice([-1, -2, 4]))
+        cfg = wl.AgCfg(world=world, shard_rows=shard, K=K, N=N)
+        _say(f"ag_gemm random case={case} world={world} M={cfg.M} N={N} K={K} grid={grid} prod={prod}")
+        A, B, order = wl.ag_inputs(cfg, seed=300 + case)
+        Ad, Bd = A.to(dev), B.to(dev)
+        A_full = torch.zeros_like(Ad)
+        flags = torch.zeros(cfg.M // 128, dtype=torch.int32, device=dev)
+        counters = torch.zeros_like(flags)
+        C = torch.empty((cfg.M, N), dtype=torch.bfloat16, device=dev)
+        ops.ag_gemm(Ad, A_full, Bd, C, flags, torch.from_numpy(order).to(dev), epoch=3, num_producers=prod,
+                    num_cus=grid, stage_counters=counters)
+        # the same number of compute workgroups (dedicated producers take
+        # grid slots), hence the same K-split plan
+        compute = (grid or ops.cu_count()) - max(prod, 0)
+        C2 = torch.empty_like(C)
+        ops.ag_gemm(None, A_full, Bd, C2, None, None, epoch=1, gated=False, num_producers=0, num_cus=compute)
+        torch.cuda.synchronize()
+        assert torch.equal(A_full.cpu(), A), f"case {case}: staging"
+        assert (flags.cpu() == 3).all(), f"case {case}: flags"
+        assert torch.equal(C.cpu(), C2.cpu()), f"case {case}: gated != ungated"
+        assert rel_fro(C.float(), ag_gemm_ref(A, B)) < TOL, f"case {case}"
+
+
 def test_ag_gemm_epochs_and_orders(dev):
     """Several calls with increasing (and skipped) epochs, different stage
     orders and both staging modes, no flag or counter reset in between:
