@@ -339,6 +339,48 @@ def test_gemm_rs_vs_oracle(dev, rank, producers, num_cus, K):
         assert torch.equal(recv.cpu(), peers)
 
 
+def test_gemm_rs_random_shapes_and_grids(dev):
+    """Seeded random reduce-scatter shapes, ranks, grids and staging modes:
+    the owned slice matches the oracle (fp32 fold, one rounding), the
+    non-owned rows are the local partials, the owned rows are not sent, and
+    staged partials are bit-exact copies."""
+    rng = np.random.default_rng(91)
+    for case in range(8):
+        world = int(rng.choice([2, 4, 8]))
+        rank = int(rng.integers(0, world))
+        M = world * int(rng.integers(1, 5)) * 256
+        N = int(rng.integers(1, 9)) * 256
+        K = int(rng.integers(1, 17)) * 64
+        grid = int(rng.choice([0, 0, 16, 64, 136]))
+        prod = int(rng.choice([-1, 0, 4]))
+        _say(f"gemm_rs random case={case} world={world} rank={rank} M={M} N={N} K={K} grid={grid} prod={prod}")
+        cfg = wl.RsCfg(world=world, rank=rank, M=M, K=K, N=N)
+        A, B, peers, order = wl.rs_inputs(cfg, seed=400 + case)
+        rows = M // world
+        nfl = (world - 1) * rows // 128
+        work = torch.zeros((M, N), dtype=torch.bfloat16, device=dev)
+        out = torch.zeros((rows, N), dtype=torch.bfloat16, device=dev)
+        if prod:
+            recv = torch.zeros_like(peers, device=dev)
+            flags = torch.zeros(nfl, dtype=torch.int32, device=dev)
+        else:
+            recv = peers.to(dev)
+            flags = torch.full((nfl,), 5, dtype=torch.int32, device=dev)
+        counters = torch.zeros(nfl, dtype=torch.int32, device=dev)
+        ops.gemm_rs(A.to(dev), B.to(dev), work, out, peers.to(dev), recv, world, rank, flags,
+                    torch.from_numpy(order).to(dev), epoch=5, num_producers=prod, stage_counters=counters,
+                    num_cus=grid)
+        torch.cuda.synchronize()
+        P, owned = gemm_rs_ref(A, B, peers, rank, world)
+        assert rel_fro(out.float(), owned) < TOL, f"case {case}: owned slice"
+        mask = torch.ones(M, dtype=torch.bool)
+        mask[rank * rows:(rank + 1) * rows] = False
+        assert rel_fro(work.cpu()[mask].float(), P[mask]) < TOL, f"case {case}: sends"
+        assert (work.cpu()[~mask] == 0).all(), f"case {case}: owned rows sent"
+        if prod:
+            assert torch.equal(recv.cpu(), peers), f"case {case}: staging"
+
+
 @pytest.mark.parametrize("world,rank,M,num_cus", [(8, 3, 4096, 0), (4, 0, 2048, 8), (8, 7, 4096, 16), (2, 1, 1024, 0)])
 def test_gemm_rs_spread_schedule_orders(dev, world, rank, M, num_cus):
     """Owned row tiles run one per round in the arrival order of their peer
