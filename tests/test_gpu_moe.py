@@ -401,3 +401,46 @@ def test_gemm1_swiglu_split_tail_exchange(dev):
     assert rel_fro(outs[0].float().cpu(), ref_act) < TOL
     assert torch.equal(outs[0], outs[1])
     assert torch.allclose(outs[0].float(), outs[2].float(), rtol=2 ** -6, atol=1e-3)
+
+
+def test_ffn_combine_random_layers(dev):
+    """Seeded random MoE layers: token count, hidden and FFN widths, expert
+    count, top-k, expert-parallel size, rank, routing skew, fused or separate
+    dispatch, tile width.  y_expert and y match the oracle, rows the rank
+    does not route stay zero, and a second run is byte-identical."""
+    rng = np.random.default_rng(1234)
+    for case in range(8):
+        experts = int(rng.choice([16, 32, 64]))
+        ep = int(rng.choice([1, 2, 4, 8]))
+        cfg = wl.MoeCfg(tokens=int(rng.integers(1, 9)) * 96, H=int(rng.integers(1, 5)) * 256,
+                        I=int(rng.integers(1, 5)) * 128, experts=experts, topk=int(rng.integers(1, 9)), ep=ep,
+                        rank=int(rng.integers(0, ep)), zipf_s=float(rng.choice([0.0, 1.1, 2.0])))
+        fuse = bool(rng.integers(0, 2))
+        tile_n = int(rng.choice([0, 256]))
+        _say(f"moe random case={case} {cfg} fuse={fuse} tile_n={tile_n}")
+        tokens, ids, gates, w1, w2 = wl.moe_inputs(cfg, seed=500 + case)
+        idx = ops.moe_build_indices(ids, gates, cfg.e0, cfg.n_local)
+        d = {k: torch.from_numpy(np.ascontiguousarray(v)).to(dev) for k, v in idx.items()
+             if isinstance(v, np.ndarray)}
+        R_pad = idx["R_pad"]
+        post = None if fuse else torch.empty((R_pad, cfg.H), dtype=torch.bfloat16, device=dev)
+        act = torch.empty((R_pad, cfg.I), dtype=torch.bfloat16, device=dev)
+        ye = torch.empty((R_pad, cfg.H), dtype=torch.bfloat16, device=dev)
+        ys = []
+        for _ in range(2):
+            y = torch.full((cfg.tokens, cfg.H), 7.0, dtype=torch.float32, device=dev)
+            ops.moe_ffn_combine(tokens.to(dev), d["pull_indices"], d["row_weight"], d["owner_offset"],
+                                d["slot_to_row"], w1.to(dev), w2.to(dev), post, act, ye, y,
+                                rb_expert=d["rb_expert"], rb_rows=d["rb_rows"], fuse_dispatch=fuse, tile_n=tile_n)
+            torch.cuda.synchronize()
+            ys.append(y.cpu())
+        assert torch.equal(ys[0], ys[1]), f"case {case}: not deterministic"
+        post_ref = om.permute_ref(tokens, idx["pull_indices"])
+        _, ye_ref = om.ffn_ref(post_ref, w1, w2, idx["padded_tokens_per_expert"], cfg.I)
+        y_ref = om.combine_ref(ye_ref, idx["row_weight"], idx["pull_indices"], cfg.tokens)
+        if idx["R"] > 0:
+            real = torch.from_numpy(np.asarray(idx["pull_indices"])[:, 2] >= 0)
+            assert rel_fro(ye.cpu().float()[real], ye_ref[real]) < TOL, f"case {case}: y_expert"
+            assert rel_fro(ys[0], y_ref) < TOL, f"case {case}: y"
+        routed = torch.from_numpy(np.diff(np.asarray(idx["owner_offset"])) > 0)
+        assert (ys[0][~routed] == 0).all(), f"case {case}: unrouted tokens"
