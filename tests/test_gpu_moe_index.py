@@ -205,3 +205,20 @@ def test_layer_graph_replays(dev, split):
         # eager library work between replays
         ops.gemm(tokens[:256], w1[0, :, :256].contiguous())
         torch.cuda.synchronize()
+
+
+def test_index_dev_random_routings(dev):
+    """Seeded random routings: token count, top-k, expert count, local
+    expert window and row block; every table bit-identical to the host
+    builder."""
+    rng = np.random.default_rng(4321)
+    for case in range(12):
+        T = int(rng.integers(1, 9000))
+        topk = int(rng.integers(1, 10))
+        experts = int(rng.choice([8, 64, 256, 1024]))
+        n_local = int(rng.integers(1, experts + 1))
+        e0 = int(rng.integers(0, experts - n_local + 1))
+        row_block = int(rng.choice([64, 128]))
+        _say(f"moe index dev random case={case} T={T} topk={topk} E={experts} e0={e0} n_local={n_local} rb={row_block}")
+        ids, gates = wl.zipf_routing(T, experts, min(topk, experts), float(rng.choice([0.0, 1.1])), 700 + case)
+        _check(dev, ids, gates, e0, n_local, row_block)
