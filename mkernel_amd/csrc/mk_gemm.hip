@@ -312,6 +312,11 @@ __device__ __forceinline__ u32x4_t make_rsrc_v(const void* base, uint32_t bytes)
 // VALU instruction (v_readlane / v_readfirstlane, e.g. a reloaded SGPR spill)
 // needs 5 wait states, and an LDS DMA after an SALU write of M0 needs 1.
 // Without them the load can use a stale rsrc / soffset and fetch wrong bytes.
+// M0 is listed as clobbered; the compiler reports that it does not preserve
+// a reserved register across inline asm, so it must hold nothing live here.
+// In the generated code the compiler's own M0 uses (v_writelane lane
+// selects in atomic expansions) set M0 immediately before the use, with no
+// DMA between.
 __device__ __forceinline__ void dma16(u32x4_t r, uint32_t lds_addr, uint32_t voff, uint32_t soff) {
   asm volatile("s_mov_b32 m0, %0\n\ts_nop 4\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
                :
@@ -515,7 +520,6 @@ __device__ __forceinline__ void store_tile(const GemmKParams& p, f32x16 (&acc)[C
                                            int tid, char* smem) {
   const int lane = tid & 63, wave = tid >> 6;
   const int wm = wave / C::WN, wn = wave % C::WN;
-  const int ml = lane & 31, kg = lane >> 5;
   if constexpr (EPI == kEpiStore) {
     // the 128-row expert tiles write rows read by a later kernel (GEMM2's
     // y_expert by the combine): nontemporal stores, which measured faster

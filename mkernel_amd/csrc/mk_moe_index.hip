@@ -231,8 +231,7 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(IndexKParams p) {
 // same launch; it writes every row's expert and the padding rows only, so
 // the two parts never write the same field).
 __global__ __launch_bounds__(kChunk) void scatter_kernel(IndexKParams p) {
-  constexpr int kWaves = kChunk / 64;
-  extern __shared__ int wcnt[];  // [kWaves][n_local]: per-wave counts of each expert
+  extern __shared__ int wcnt[];  // [kChunk / 64 waves][n_local]: per-wave counts of each expert
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const mk_moe_index& o = p.out;
   if ((int)blockIdx.x < p.nchunks) {
