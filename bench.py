@@ -426,12 +426,26 @@ def bench_moe(steps, warmup, extra):
 
 
 # ------------------------------------------------------------ CPU baseline
-def cpu_baseline_moe(inputs, tokens_per_sample: int = 1024, reps: int = 3) -> dict:
+def _timed_reps(fn, budget_s: float, max_reps: int = 1000):
+    """Run fn repeatedly (after one untimed call) until budget_s of measured
+    time has passed; returns (reps, seconds)."""
+    fn()
+    reps, total = 0, 0.0
+    while total < budget_s and reps < max_reps:
+        t0 = time.perf_counter()
+        fn()
+        total += time.perf_counter() - t0
+        reps += 1
+    return reps, total
+
+
+def cpu_baseline_moe(inputs, tokens_per_sample: int = 1024, budget_s: float = 10.0) -> dict:
     """Config 5's layer in float32 torch on the host cores, on a bounded
     sample: the first `tokens_per_sample` tokens of the same routing, their
     routed rows gathered with index_select, per-expert matmul, F.silu(g) * u,
-    matmul, gate-weighted index_add_ back to token order.  Tokens/s of the
-    sample (the work scales with the routed rows)."""
+    matmul, gate-weighted index_add_ back to token order, repeated for about
+    budget_s seconds.  Tokens/s of the sample (the work scales with the
+    routed rows)."""
     import torch.nn.functional as F
     cfg = wl.MoeCfg()
     tokens, ids, gates, w1, w2 = (t.cpu() if torch.is_tensor(t) else t for t in inputs)  # the GPU run's inputs
@@ -457,36 +471,29 @@ def cpu_baseline_moe(inputs, tokens_per_sample: int = 1024, reps: int = 3) -> di
             y.index_add_(0, src.index_select(0, sel), wts.index_select(0, sel)[:, None] * ye)
         return y
 
-    layer()
-    times = []
-    for _ in range(reps):
-        t0 = time.perf_counter()
-        layer()
-        times.append(time.perf_counter() - t0)
-    t = statistics.median(times)
+    reps, total = _timed_reps(layer, budget_s)
+    t = total / reps
     return {"value": T / t, "unit": "tokens/s", "cores": torch.get_num_threads(), "cpu_count": os.cpu_count(),
             "kind": "port",
             "sample": f"first {T} of 4096 tokens ({int(real.sum())} routed rows), fp32 torch on CPU: index_select, "
-                      f"per-expert matmul, F.silu(g)*u, matmul, weighted index_add_; median of {reps}",
+                      f"per-expert matmul, F.silu(g)*u, matmul, weighted index_add_; {reps} repetitions, "
+                      f"{total:.1f} s of CPU work",
             "seconds": t}
 
 
-def cpu_baseline(A_full, B, rows: int = 256, reps: int = 3):
+def cpu_baseline(A_full, B, rows: int = 2048, budget_s: float = 10.0):
     """The oracle's float32 torch matmul on the host cores, on a bounded
-    sample of the same workload: `rows` rows of A_full times B."""
+    sample of the same workload: `rows` rows of A_full (one shard) times B,
+    repeated for about budget_s seconds."""
     from oracle.gemm import gemm_ref  # CPU baseline leg only
     torch.set_num_threads(os.cpu_count() or 1)
     a = A_full[:rows].cpu()
     b = B.cpu()
-    times = []
-    for _ in range(reps):
-        t0 = time.perf_counter()
-        gemm_ref(a, b)
-        times.append(time.perf_counter() - t0)
-    t = statistics.median(times)
-    flops = 2.0 * rows * b.shape[0] * b.shape[1]
-    return {"value": flops / t / 1e12, "unit": "TFLOP/s", "cores": torch.get_num_threads(), "kind": "port",
-            "sample": f"A_full[:{rows}] @ B ({rows}x{b.shape[0]}x{b.shape[1]}, fp32 torch on CPU), median of {reps}"}
+    reps, total = _timed_reps(lambda: gemm_ref(a, b), budget_s)
+    flops = 2.0 * rows * b.shape[0] * b.shape[1] * reps
+    return {"value": flops / total / 1e12, "unit": "TFLOP/s", "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"A_full[:{rows}] @ B ({rows}x{b.shape[0]}x{b.shape[1]}, one shard, fp32 torch on CPU), "
+                      f"{reps} repetitions, {total:.1f} s of CPU work"}
 
 
 def load_traffic():
