@@ -393,7 +393,7 @@ int mk_ag_gemm(const mk_ag_gemm_args* a, void* stream) {
 
 
 int mk_ag_gemm_noalloc(const mk_ag_gemm_args* a, void* stream) {
-  if (!a) return fail(MK_EINVAL, "mk_ag_gemm_noalloc: null argument");
+  if (!a || !a->A_full || !a->B || !a->C) return fail(MK_EINVAL, "mk_ag_gemm_noalloc: null argument");
   if (a->split_ws || a->split_ws_bytes || a->stage_counters)
     return fail(MK_EINVAL, "mk_ag_gemm_noalloc: split_ws and stage_counters come from the library's static scratch; "
                            "pass them as NULL / 0");
@@ -902,6 +902,14 @@ int mk_moe_build_indices_dev(const mk_moe_index_dev_args* a, void* stream) {
 
 int mk_moe_ffn_combine(const mk_moe_ffn_args* a, void* stream) {
   if (!a) return fail(MK_EINVAL, "mk_moe_ffn_combine: null argument");
+  // every buffer the sequence touches, before anything is queued (buffers
+  // of no rows may be NULL)
+  const bool rows = a->R_pad > 0;
+  if ((rows && (!a->tokens || !a->pull_indices || !a->w1 || !a->w2 || !a->act || !a->y_expert || !a->row_weight ||
+                !a->slot_to_row || (!a->rb_expert && !a->padded_tokens_per_expert) ||
+                (!a->fuse_dispatch && !a->post_tokens))) ||
+      (a->num_tokens > 0 && (!a->owner_offset || !a->y_out)))
+    return fail(MK_EINVAL, "mk_moe_ffn_combine: null argument");
   if (a->I % 128) return fail(MK_ESHAPE, "mk_moe_ffn_combine: I must be a multiple of 128");
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (a->fuse_dispatch) {

@@ -94,3 +94,26 @@ def test_index_builder_matches_oracle(T, rank):
 def test_index_builder_rejects_bad_args():
     with pytest.raises(capi.MkError):
         ops.moe_build_indices(np.zeros((4, 2), np.int32), np.zeros((4, 2), np.float32), 0, 0)
+
+
+_ARGS_ENTRIES = {"mk_gemm": capi.GemmArgs, "mk_ag_gemm": capi.AgGemmArgs, "mk_ag_gemm_noalloc": capi.AgGemmArgs,
+                 "mk_gemm_rs": capi.GemmRsArgs, "mk_gemm_ar": capi.GemmArArgs, "mk_gemm_ar_two_shot": capi.GemmAr2Args,
+                 "mk_moe_permute": capi.MoePermuteArgs, "mk_moe_grouped_gemm": capi.MoeGroupedGemmArgs,
+                 "mk_moe_combine": capi.MoeCombineArgs, "mk_moe_ffn_combine": capi.MoeFfnArgs,
+                 "mk_moe_build_indices_dev": capi.MoeIndexDevArgs}
+
+
+@pytest.mark.parametrize("name", sorted(_ARGS_ENTRIES))
+def test_entry_points_refuse_missing_arguments(name):
+    """Every args-struct entry point refuses a NULL struct (a negative code,
+    i.e. an argument error and not a HIP error, with a message naming the
+    entry point) and a zero-filled struct (NULL operands, zero sizes), both
+    before touching a device: this container has none, so any device call
+    would return a positive HIP error instead."""
+    L = capi.lib()
+    L.mk_last_error_string.restype = C.c_char_p
+    fn = getattr(L, name)
+    assert fn(None, None) < 0
+    assert name.encode() in L.mk_last_error_string()
+    empty = _ARGS_ENTRIES[name]()  # every pointer NULL, every size 0
+    assert fn(C.byref(empty), None) < 0, L.mk_last_error_string()
